@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused Screening Attention hot path on one MI355X.
+
+Workload: one screening-attention layer core,
+forward + backward, bf16, B=4, T=8192, H=8, head_dim=64, causal;
+q/k/v ~ N(0,1) in the projection layout (B,T,H,D); r_h ~ U[1.9,2.1];
+w_h ~ U[256,8192]; dO ~ N(0,1).  A step is one fused forward (msa_fwd) plus
+one fused backward (msa_bwd, incl. dr/dw) over that batch, inputs resident in
+HBM.  value = tokens/s = B*T / step time.
+
+Also reported:
+  roofline      the dominant kernel (by measured time) against its bound
+  cpu_baseline  the reference's dense torch-fp32 math on the host cores, on a
+                bounded sample, scaled to the same unit
+  decode        the T=100K single-query decode kernel (configs[4] shape) in
+                GB/s against HBM peak
+Prints ONE JSON line.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "pytorch-implementation-of-screening-attention_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+TILE_FLOP = 2 * 64 * 64 * 64  # one 64x64 tile product with D=64
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+def window_tiles(T, w_list, tile=64):
+    """|W|: causal 64x64 tiles holding a pair with 0 <= i-j < w, per (b,h) summed over heads."""
+    n = 0
+    nt = (T + tile - 1) // tile
+    for w in w_list:
+        wc = min(int(math.ceil(w)), 10 ** 9)
+        for qt in range(nt):
+            q0 = qt * tile
+            qlast = min(q0 + tile - 1, T - 1)
+            jlo = max(0, q0 - wc + 1)
+            n += qlast // tile - jlo // tile + 1
+    return n
+
+
+def popcount_bits(bits):
+    import torch
+    b = bits.to(torch.int64) & 0xFFFFFFFF
+    c = torch.zeros_like(b)
+    for s in range(32):
+        c += (b >> s) & 1
+    return int(c.sum())
+
+
+def kernel_times(L, kid, fn, n):
+    """Average duration (ms) of kernel `kid` over n calls of fn, via HIP events."""
+    import ctypes
+    assert L.msa_timer_arm(kid, n) == 0
+    for _ in range(n):
+        fn()
+    buf = (ctypes.c_float * n)()
+    got = L.msa_timer_read(buf, n)
+    L.msa_timer_arm(0, 0)
+    vals = [buf[i] for i in range(got)]
+    return sum(vals) / max(1, len(vals)), vals
+
+
+def cpu_baseline(B, T, H, D, r, w, seed):
+    """Dense reference math (torch fp32) fwd+bwd on 1 (b,h) slice of the workload."""
+    import torch
+    sys.path.insert(0, os.path.join(HERE, "oracle"))
+    import cpu_torch
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    Ts = T
+    g = torch.Generator().manual_seed(seed + 100)
+    q, k, v, dy = (torch.randn(1, Ts, 1, D, generator=g).bfloat16().float() for _ in range(4))
+    rr, ww = torch.tensor([r[0]]), torch.tensor([w[0]])
+    cpu_torch.fwd_bwd(q[:, :512], k[:, :512], v[:, :512], rr, ww, dy[:, :512])  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        cpu_torch.fwd_bwd(q, k, v, rr, ww, dy)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    # the full workload is B*H independent slices of this size
+    full = t * B * H
+    return {"value": B * T / full, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/cpu_torch.py dense fp32 fwd+bwd of one (b,h) slice, T={Ts}, D={D}, "
+                      f"median of 3 = {t:.3f} s, scaled x{B * H} slices to B={B},H={H}",
+            "cpu": _cpu_name()}
+
+
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def decode_bench(L, ops, torch, steps=20):
+    """configs[4] attention shape: B=16, cache 100,000 positions, H=8, D=64, bf16.
+    Decode-stream variant: w_h = 1e5 for all heads (the whole cache is in window)."""
+    B, Tc, H, D = 16, 100000, 8, 64
+    g = torch.Generator(device="cuda").manual_seed(5)
+    kc = torch.randn(B, Tc, H, D, device="cuda", generator=g).bfloat16()
+    vc = torch.randn(B, Tc, H, D, device="cuda", generator=g).bfloat16()
+    q = torch.randn(B, H, D, device="cuda", generator=g).bfloat16()
+    r = torch.full((H,), 2.0, device="cuda")
+    w = torch.full((H,), 1e5, device="cuda")
+    ws = torch.empty(int(L.msa_decode_workspace_bytes(B, H, D, Tc)), dtype=torch.uint8, device="cuda")
+    fn = lambda: ops.decode_step(q, kc, vc, Tc, r, w, 1e-8, ws)
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ms, _ = kernel_times(L, 7, fn, steps)
+    torch.cuda.synchronize()
+    bytes_k = B * H * Tc * D * 2
+    # V rows are read only for live keys; count them exactly on the GPU
+    qn = torch.nn.functional.normalize(q.float(), dim=-1)
+    kn = torch.nn.functional.normalize(kc.float(), dim=-1)
+    live = 0
+    for b in range(B):
+        s = torch.einsum("hd,thd->th", qn[b], kn[b])
+        live += int((1.0 - 2.0 * (1.0 - s) > 0).sum())
+    bytes_v = live * D * 2
+    gbs = (bytes_k + bytes_v) / (ms * 1e-3) / 1e9
+    return {"workload": "decode B=16, cache 100000, H=8, D=64, bf16, w=1e5 (decode-stream variant)",
+            "kernel": "decode_partial_kernel", "ms": round(ms, 4), "bytes": bytes_k + bytes_v,
+            "live_v_rows": live, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (every box here has one); --gpus {args.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from multiscreen import _native, ops
+    L = _native.lib()
+    torch.manual_seed(args.seed)
+    dev = torch.device("cuda:0")
+
+    B, T, H, D = 4, 8192, 8, 64
+    g = torch.Generator().manual_seed(args.seed)
+    r = (1.9 + 0.2 * torch.rand(H, generator=g)).tolist()
+    w = (256.0 + (8192.0 - 256.0) * torch.rand(H, generator=g)).tolist()
+    gd = torch.Generator(device="cuda").manual_seed(args.seed)
+    q, k, v, dy = (torch.randn(B, T, H, D, device=dev, generator=gd).bfloat16() for _ in range(4))
+    rg = torch.tensor(r, device=dev)
+    wg = torch.tensor(w, device=dev)
+
+    def step():
+        y, hnorm, bits, ws = ops.fwd_raw(q, k, v, rg, wg, True, 1e-8, None, need_bwd=True)
+        grads = ops.bwd_raw(q, k, v, rg, wg, True, 1e-8, y, hnorm, bits, ws, dy)
+        return bits
+
+    for _ in range(args.warmup):
+        bits = step()
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` steps, synchronised on both sides; the
+    # forward kernel's own launches are bracketed by HIP events on its stream
+    import ctypes
+    assert L.msa_timer_arm(2, args.steps) == 0
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(args.steps):
+        bits = step()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = t0.elapsed_time(t1) / args.steps
+    buf = (ctypes.c_float * args.steps)()
+    n = L.msa_timer_read(buf, args.steps)
+    L.msa_timer_arm(0, 0)
+    fwd_ms = sum(buf[i] for i in range(n)) / max(1, n)
+
+    # per-kernel breakdown (outside the timed region)
+    breakdown = {"fwd_kernel": fwd_ms}
+    for kid, name in ((1, "prep_kv_kernel"), (3, "bwd_prep_kernel"), (4, "dkdv_kernel"),
+                      (5, "dq_kernel"), (6, "rw_reduce_kernel")):
+        breakdown[name] = kernel_times(L, kid, step, 5)[0]
+    torch.cuda.synchronize()
+
+    nW = window_tiles(T, w) * B
+    nA = popcount_bits(bits)
+    f_fwd = TILE_FLOP * (nW + nA)
+    f_total = TILE_FLOP * (nW + 6 * nA)
+    dom = max(breakdown, key=breakdown.get)
+    dom_flop = {"fwd_kernel": f_fwd, "dkdv_kernel": TILE_FLOP * 4 * nA,
+                "dq_kernel": TILE_FLOP * 3 * nA}.get(dom)
+    achieved = dom_flop / (breakdown[dom] * 1e-3) / 1e12 if dom_flop else None
+    tokens_s = B * T / (ms_step * 1e-3)
+    step_tflops = f_total / (ms_step * 1e-3) / 1e12
+
+    out = {
+        "metric": "screening-attn fwd+bwd tokens/s at T=8K (% bf16 MFMA peak); T=100K decode GB/s",
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v/dO; r~U[1.9,2.1], w~U[256,8192])",
+        "config": {"workload": "configs[1]: screening-attention core fwd+bwd, B=4 T=8192 H=8 D=64 causal",
+                   "global_batch": B, "seq_len": T, "heads": H, "head_dim": D,
+                   "r": [round(x, 4) for x in r], "w": [round(x, 1) for x in w]},
+        "roofline": {"bound": "mfma", "kernel": dom,
+                     "achieved": round(achieved, 2) if achieved else None,
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 5) if achieved else None,
+                     "traffic": None,
+                     "flop_per_launch": dom_flop},
+        "tiles": {"causal": B * H * (T // 64) * (T // 64 + 1) // 2, "window": nW, "active": nA,
+                  "window_skip": round(1 - nW / (B * H * (T // 64) * (T // 64 + 1) / 2), 4),
+                  "threshold_skip": round(1 - nA / nW, 5)},
+        "step_tflops_alg": round(step_tflops, 2),
+        "step_frac_bf16_peak": round(step_tflops / PEAK_BF16_TFLOPS, 5),
+        "kernel_ms": {k_: round(v_, 4) for k_, v_ in breakdown.items()},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_decode:
+        out["decode"] = decode_bench(L, ops, torch)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, T, H, D, r, w, args.seed)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

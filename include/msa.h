@@ -1,0 +1,166 @@
+/*
+ * msa.h -- C ABI of the MI355X (gfx950) fused Screening Attention library
+ * (libmsa.so).  Plain pointers, sizes and a hipStream_t passed as void*; no
+ * torch or C++ types cross this boundary.
+ *
+ * The math is that of the reference's dense path
+ *   /root/reference/multiscreen/attention.py:142-200 and norm.py:23-25:
+ *     q^ = q/max(|q|,eps)   k^, v^ likewise                (attention.py:155-158)
+ *     s_ij = q^_i . k^_j                                      (attention.py:160-161)
+ *     a_ij = relu(1 - r_h (1 - s_ij)),  alpha_ij = a_ij^2      (attention.py:75-90)
+ *     m_ij = (cos(pi (j-i)/w_h) + 1)/2 on -w<j-i<=0 (causal)   (attention.py:92-119)
+ *            or on |j-i|<w (non-causal)                        (attention.py:174-183)
+ *     alpha_ij = 0 where key_padding_mask[b,j]                 (attention.py:185-188)
+ *     h_i = sum_j alpha_ij m_ij v^_j      (no normaliser)      (attention.py:192-193)
+ *     y_i = tanh(n_i)/n_i h_i, n_i = max(|h_i|, eps)           (norm.py:23-25)
+ *
+ * Tensor conventions
+ *   q,k,v   : raw projections viewed as (B, T, H, D) with element strides
+ *             (sb, st, sh) and unit stride over D -- exactly the
+ *             proj(x).view(B,T,H,D) view the reference builds before its
+ *             transpose (attention.py:150-153).  Strides and base pointers
+ *             must allow 16-byte vector loads (strides multiple of 8 elements
+ *             for bf16, of 4 for fp32).
+ *   y, dy, dq, dk, dv : contiguous (B, T, H, D), i.e. the (B,T,d_model) layout
+ *             out_proj consumes (attention.py:198-200).
+ *   r, w    : fp32 (H,), r = exp(s_r)+1, w = exp(s_v)+1 (attention.py:164-165).
+ *   key_padding_mask : nullable uint8 (B, Tk), nonzero = ignore key.
+ *   dtype   : MSA_F32 or MSA_BF16 for q,k,v,y,dy,dq,dk,dv.
+ *
+ * Ownership: the caller allocates every buffer (outputs and workspaces); the
+ * library never allocates or frees device memory.  Every call is
+ * stream-ordered on `stream` and does not synchronise the host.
+ * Errors: a nonzero return code; msa_last_error() gives a thread-local
+ * description.  Argument validation runs on the host before any HIP call.
+ */
+#ifndef MSA_H
+#define MSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum msa_dtype { MSA_F32 = 0, MSA_BF16 = 1 };
+
+enum msa_status {
+  MSA_OK = 0,
+  MSA_ERR_INVALID = 1,   /* bad shape / dtype / stride / pointer / size    */
+  MSA_ERR_WORKSPACE = 2, /* workspace or bitmap buffer too small            */
+  MSA_ERR_HIP = 3        /* a HIP runtime call or kernel launch failed      */
+};
+
+/* Library version, (major<<16)|(minor<<8)|patch. */
+int msa_version(void);
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* msa_last_error(void);
+
+/* Bytes of forward workspace: normalised K^/V^ copies in the layouts the
+ * kernels read.  need_bwd=1 adds the copies the backward reads; the same
+ * workspace must then be handed unchanged to msa_bwd. */
+size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype,
+                               int need_bwd);
+
+/* Number of uint32 words of the active-tile bitmap: one bit per
+ * (b, h, 64-query tile, 64-key tile), set iff some in-window, unmasked pair of
+ * the tile has alpha > 0. */
+size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);
+
+/* Bytes of backward workspace. */
+size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
+
+/*
+ * Fused forward.  Replaces, as one call, what the reference's fused boundary
+ * does across torch and Triton:
+ *   F.normalize x3        attention_triton.py:115-117
+ *   _ScreeningFunc.forward / screening_attention_fwd
+ *                         attention_triton.py:31-36, screening_fwd.py:216-270
+ *   TanhNorm + merge      attention_triton.py:135-137
+ * and adds key_padding_mask (attention.py:185-188), which the Triton path
+ * ignores (attention_triton.py:125-132).
+ * Outputs: y (B,Tq,H,D) = TanhNorm(h); hnorm (B,H,Tq) fp32 = |h_i| before the
+ * eps clamp (needed by msa_bwd); tile_bits (msa_tile_bits_words words).
+ */
+int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+            const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+            const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+            int B, int H, int Tq, int Tk, int D, int dtype,
+            const float* r, const float* w, const uint8_t* key_padding_mask,
+            int causal, float eps,
+            void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words,
+            void* workspace, size_t workspace_bytes, int need_bwd,
+            void* stream);
+
+/*
+ * Fused backward.  Replaces _ScreeningFunc.backward / screening_attention_bwd
+ * (attention_triton.py:38-44, screening_bwd.py:229-287) together with the
+ * torch autograd of F.normalize and TanhNorm around it, and -- unlike the
+ * reference fused path, which returns None for them (attention_triton.py:44)
+ * -- produces the per-head gradients dr, dw (H,) that attention.py's autograd
+ * delivers to s_r / s_v through r = exp(s_r)+1, w = exp(s_v)+1.
+ * dq (B,Tq,H,D), dk, dv (B,Tk,H,D) are written in full (zeros where no
+ * active pair reaches a row).  Deterministic: no atomics.
+ * fwd_workspace is the one filled by msa_fwd with need_bwd=1.
+ */
+int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+            const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+            const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+            int B, int H, int Tq, int Tk, int D, int dtype,
+            const float* r, const float* w, int causal, float eps,
+            const void* y, const float* hnorm, const void* dy,
+            const uint32_t* tile_bits, size_t tile_bits_words,
+            const void* fwd_workspace, size_t fwd_workspace_bytes,
+            void* dq, void* dk, void* dv, float* dr, float* dw,
+            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of decode workspace (split-key partial sums). */
+size_t msa_decode_workspace_bytes(int B, int H, int D, int max_len);
+
+/*
+ * Single-query decode against a KV cache.  The reference has no KV cache: its
+ * MultiscreenLM.generate re-runs the full forward over the prefix for every
+ * token and keeps only the last row (model.py:111-141).  This computes that
+ * last row directly: the query at position pos = cache_len-1 attends to the
+ * causal window (pos - w, pos] of the cache, which already holds the new
+ * token's k and v.
+ *   q      : (B, H, D) raw query projection, strides (q_sb, q_sh), unit D.
+ *   kcache, vcache : (B, Tcap, H, D) raw k/v projections, strides (sb, st, sh);
+ *            cache_cap = Tcap, and 1 <= cache_len <= cache_cap.
+ *   y      : (B, H, D) contiguous, TanhNorm(h).
+ */
+int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
+               const void* kcache, int64_t k_sb, int64_t k_st, int64_t k_sh,
+               const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh,
+               int B, int H, int D, int dtype, int cache_len, int cache_cap,
+               const float* r, const float* w, float eps,
+               void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel timing for measurement.  After msa_timer_arm(kernel, n) the next n
+ * launches of that kernel (any entry point) each record a HIP event pair on
+ * their stream around the launch; msa_timer_read waits for the recorded
+ * pairs and writes their durations in milliseconds, returning how many were
+ * recorded.  msa_timer_arm(0, 0) disarms.  Process-wide; not for concurrent
+ * use from several threads. */
+enum msa_kernel_id {
+  MSA_K_PREP_KV = 1, MSA_K_FWD = 2, MSA_K_BWD_PREP = 3, MSA_K_DKDV = 4,
+  MSA_K_DQ = 5, MSA_K_RW_REDUCE = 6, MSA_K_DECODE = 7
+};
+int msa_timer_arm(int kernel, int n);
+int msa_timer_read(float* ms, int n);
+
+/* Device self-test of the MFMA operand layouts the kernels assume: writes the
+ * 32x32 products A.B (bf16 32x32x16 and fp32 32x32x2 forms) of the given
+ * row-major fp32 inputs a (32xK) and b (Kx32), K=16 and K=2, to out16, out2
+ * (each 32x32 fp32, row-major).  Test infrastructure only. */
+int msa_selftest_mfma(const float* a16, const float* b16, float* out16,
+                      const float* a2, const float* b2, float* out2,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSA_H */

@@ -1,0 +1,287 @@
+"""CPU oracle for the fused Screening Attention path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
+this module, and only as the checker (or the timed CPU baseline), never as a
+code path of the product.
+
+A float64 numpy restatement of the reference's dense algorithm,
+/root/reference/multiscreen/attention.py and norm.py:
+
+  normalize       attention.py:155-158  x / max(|x|, eps)   (F.normalize)
+  similarity      attention.py:160-161  s = q^ k^T
+  trim-and-square attention.py:75-90    relu(1 - r(1-s))^2
+  softmask        attention.py:92-119   causal:  (cos(pi(j-i)/w)+1)/2 on -w<j-i<=0
+                  attention.py:174-183  non-causal: same on |j-i| < w
+  key padding     attention.py:185-188  alpha[b,:,:,j] = 0 where mask
+  aggregate       attention.py:192-193  h = alpha v^   (no normaliser)
+  TanhNorm        norm.py:23-25         tanh(n)/n h,  n = max(|h|, eps)
+  per-head params attention.py:164-165  w = exp(s_v)+1, r = exp(s_r)+1
+
+plus the analytic backward of the same map (the reference leaves it to torch
+autograd; its fused Triton backward states the normalised-operand formulas in
+screening_bwd.py:6-18 and drops dr/dw, attention_triton.py:44).
+
+Tensor convention: q (B,Tq,H,D), k/v (B,Tk,H,D) -- the raw projections as the
+(B,T,H,D) view of attention.py:150-151 -- and r, w (H,).  Query rows are
+processed in blocks so memory stays O(block * Tk) at any length.
+
+Pinning (tests/test_oracle.py): closed-form known answers (one-hot q=k, the
+head-0 init window w=2, below-threshold zeros, TanhNorm properties), a
+pure-Python per-pair brute force on tiny inputs, central finite differences
+for every gradient, torch.autograd of an independent torch restatement, and
+the golden vectors written from the reference module (tests/golden/).
+"""
+
+import math
+
+import numpy as np
+
+EPS = 1e-8
+
+
+def normalize(x, eps=EPS):
+    """x / max(|x|, eps) over the last axis (F.normalize, attention.py:156-158)."""
+    n = np.sqrt(np.sum(x * x, axis=-1, keepdims=True))
+    return x / np.maximum(n, eps)
+
+
+def trim_and_square(s, r):
+    """relu(1 - r(1-s))^2 (attention.py:75-90); r broadcasts against s."""
+    a = np.maximum(1.0 - r * (1.0 - s), 0.0)
+    return a * a
+
+
+def softmask(qpos, kpos, w, causal):
+    """(H, len(qpos), len(kpos)) window-cut cosine mask (attention.py:92-119, :174-183)."""
+    rel = (kpos[None, :] - qpos[:, None]).astype(np.float64)[None]   # j - i
+    w = np.asarray(w, dtype=np.float64).reshape(-1, 1, 1)
+    m = 0.5 * (np.cos(math.pi * rel / w) + 1.0)
+    inside = ((rel > -w) & (rel <= 0)) if causal else (np.abs(rel) < w)
+    return m * inside
+
+
+def softmask_dw(qpos, kpos, w, causal):
+    """d softmask / d w on in-window pairs (0 elsewhere)."""
+    rel = (kpos[None, :] - qpos[:, None]).astype(np.float64)[None]
+    w = np.asarray(w, dtype=np.float64).reshape(-1, 1, 1)
+    d = 0.5 * np.sin(math.pi * rel / w) * math.pi * rel / (w * w)
+    inside = ((rel > -w) & (rel <= 0)) if causal else (np.abs(rel) < w)
+    return d * inside
+
+
+def _heads(x):
+    """(B,T,H,D) -> (B,H,T,D) float64."""
+    return np.ascontiguousarray(np.transpose(np.asarray(x, dtype=np.float64), (0, 2, 1, 3)))
+
+
+def _blocks(T, block):
+    for i0 in range(0, T, block):
+        yield i0, min(T, i0 + block)
+
+
+def forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=None, block=256,
+            q_offset=0, return_h=False):
+    """TanhNorm'd attention output y (B,Tq,H,D); optionally also h (B,H,Tq,D).
+
+    Query row t sits at position q_offset + t (0 in the reference forward).
+    """
+    qn, kn, vn = normalize(_heads(q), eps), normalize(_heads(k), eps), normalize(_heads(v), eps)
+    B, H, Tq, D = qn.shape
+    Tk = kn.shape[2]
+    r = np.asarray(r, dtype=np.float64).reshape(1, H, 1, 1)
+    kpos = np.arange(Tk)
+    h = np.zeros((B, H, Tq, D))
+    for i0, i1 in _blocks(Tq, block):
+        s = qn[:, :, i0:i1] @ np.swapaxes(kn, -1, -2)
+        p = trim_and_square(s, r) * softmask(np.arange(i0, i1) + q_offset, kpos, w, causal)[None]
+        if key_padding_mask is not None:
+            p = p * (~np.asarray(key_padding_mask, dtype=bool))[:, None, None, :]
+        h[:, :, i0:i1] = p @ vn
+    n = np.sqrt(np.sum(h * h, axis=-1, keepdims=True))
+    nc = np.maximum(n, eps)
+    y = np.tanh(nc) / nc * h
+    y = np.transpose(y, (0, 2, 1, 3))
+    return (y, h) if return_h else y
+
+
+def _tanhnorm_g(n):
+    """G(n) = F'(n)/n, F(n) = tanh(n)/n; series where the closed form cancels."""
+    n = np.asarray(n, dtype=np.float64)
+    small = n < 1e-2
+    ns = np.where(small, 1.0, n)
+    t = np.tanh(ns)
+    closed = ((1.0 - t * t) / ns - t / (ns * ns)) / ns
+    n2 = n * n
+    series = -2.0 / 3.0 + n2 * (8.0 / 15.0 + n2 * (-34.0 / 105.0 + n2 * (496.0 / 2835.0)))
+    return np.where(small, series, closed)
+
+
+def _normalize_bwd(x, dxn, eps):
+    """Gradient of x -> x/max(|x|,eps) (F.normalize) for upstream dxn."""
+    n = np.sqrt(np.sum(x * x, axis=-1, keepdims=True))
+    xn = x / np.maximum(n, eps)
+    proj = np.sum(xn * dxn, axis=-1, keepdims=True)
+    big = n > eps
+    return np.where(big, (dxn - xn * proj) / np.maximum(n, eps), dxn / eps)
+
+
+def backward(q, k, v, r, w, dy, causal=True, eps=EPS, key_padding_mask=None, block=256):
+    """Gradients (dq, dk, dv, dr, dw) of sum(y * dy) for y = forward(...)."""
+    qh, kh, vh = _heads(q), _heads(k), _heads(v)
+    qn, kn, vn = normalize(qh, eps), normalize(kh, eps), normalize(vh, eps)
+    B, H, Tq, D = qn.shape
+    Tk = kn.shape[2]
+    r1 = np.asarray(r, dtype=np.float64).reshape(1, H, 1, 1)
+    kpos = np.arange(Tk)
+    keep = None
+    if key_padding_mask is not None:
+        keep = (~np.asarray(key_padding_mask, dtype=bool))[:, None, None, :]
+
+    _, h = forward(q, k, v, r, w, causal, eps, key_padding_mask, block, return_h=True)
+    g = _heads(dy)
+    # TanhNorm backward (norm.py:24-25 with the clamp at eps)
+    n = np.sqrt(np.sum(h * h, axis=-1, keepdims=True))
+    big = n > eps
+    nc = np.maximum(n, eps)
+    F = np.tanh(nc) / nc
+    G = _tanhnorm_g(nc)
+    hd = np.sum(h * g, axis=-1, keepdims=True)
+    dh = np.where(big, F * g + G * hd * h, (math.tanh(eps) / eps) * g)
+
+    dqn = np.zeros_like(qn)
+    dkn = np.zeros_like(kn)
+    dvn = np.zeros_like(vn)
+    dr = np.zeros(H)
+    dw = np.zeros(H)
+    for i0, i1 in _blocks(Tq, block):
+        qpos = np.arange(i0, i1)
+        s = qn[:, :, i0:i1] @ np.swapaxes(kn, -1, -2)
+        a = np.maximum(1.0 - r1 * (1.0 - s), 0.0)
+        m = softmask(qpos, kpos, w, causal)[None]
+        mdw = softmask_dw(qpos, kpos, w, causal)[None]
+        if keep is not None:
+            m = m * keep
+            mdw = mdw * keep
+        p = a * a * m
+        dP = dh[:, :, i0:i1] @ np.swapaxes(vn, -1, -2)
+        dvn += np.swapaxes(p, -1, -2) @ dh[:, :, i0:i1]
+        ds = 2.0 * a * r1 * m * dP                     # a = 0 where the relu is off
+        dqn[:, :, i0:i1] = ds @ kn
+        dkn += np.swapaxes(ds, -1, -2) @ qn[:, :, i0:i1]
+        dr += np.sum(-2.0 * a * (1.0 - s) * m * dP, axis=(0, 2, 3))
+        dw += np.sum(a * a * mdw * dP, axis=(0, 2, 3))
+    dq = _normalize_bwd(qh, dqn, eps)
+    dk = _normalize_bwd(kh, dkn, eps)
+    dv = _normalize_bwd(vh, dvn, eps)
+    t = lambda x: np.transpose(x, (0, 2, 1, 3))
+    return t(dq), t(dk), t(dv), dr, dw
+
+
+def brute_force_forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=None):
+    """Pure-Python per-pair loops; tiny inputs only.  Same contract as forward()."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    B, Tq, H, D = q.shape
+    Tk = k.shape[1]
+    y = np.zeros((B, Tq, H, D))
+
+    def unit(x):
+        n = math.sqrt(sum(float(e) * float(e) for e in x))
+        return [float(e) / max(n, eps) for e in x]
+
+    for b in range(B):
+        for hh in range(H):
+            ks = [unit(k[b, j, hh]) for j in range(Tk)]
+            vs = [unit(v[b, j, hh]) for j in range(Tk)]
+            for i in range(Tq):
+                qi = unit(q[b, i, hh])
+                acc = [0.0] * D
+                for j in range(Tk):
+                    if key_padding_mask is not None and key_padding_mask[b][j]:
+                        continue
+                    rel = j - i
+                    ww = float(w[hh])
+                    inside = (-ww < rel <= 0) if causal else (abs(rel) < ww)
+                    if not inside:
+                        continue
+                    s = sum(qi[e] * ks[j][e] for e in range(D))
+                    a = max(1.0 - float(r[hh]) * (1.0 - s), 0.0)
+                    wt = a * a * 0.5 * (math.cos(math.pi * rel / ww) + 1.0)
+                    for e in range(D):
+                        acc[e] += wt * vs[j][e]
+                n = max(math.sqrt(sum(e * e for e in acc)), eps)
+                f = math.tanh(n) / n
+                for e in range(D):
+                    y[b, i, hh, e] = f * acc[e]
+    return y
+
+
+def rows_forward(q, k, v, r, w, rows, causal=True, eps=EPS):
+    """y at the listed query rows only (B,len(rows),H,D): O(len(rows)*Tk*D).
+
+    For lengths where a full oracle pass is too slow (e.g. T = 100,000)."""
+    q = np.asarray(q)[:, rows]
+    return _rows(q, k, v, r, w, np.asarray(rows), causal, eps)
+
+
+def _rows(qsel, k, v, r, w, qpos, causal, eps):
+    qn, kn, vn = normalize(_heads(qsel), eps), normalize(_heads(k), eps), normalize(_heads(v), eps)
+    B, H, R, D = qn.shape
+    Tk = kn.shape[2]
+    rr = np.asarray(r, dtype=np.float64).reshape(1, H, 1, 1)
+    h = np.zeros((B, H, R, D))
+    wmax = float(np.max(w))
+    for t, i in enumerate(qpos):
+        lo = 0 if not math.isfinite(wmax) else max(0, int(i - math.ceil(wmax)))
+        hi = Tk if not causal else min(Tk, int(i) + 1)
+        if not causal:
+            hi = Tk if not math.isfinite(wmax) else min(Tk, int(i + math.ceil(wmax)) + 1)
+        kp = np.arange(lo, hi)
+        s = qn[:, :, t:t + 1] @ np.swapaxes(kn[:, :, lo:hi], -1, -2)
+        p = trim_and_square(s, rr) * softmask(np.array([i]), kp, w, causal)[None]
+        h[:, :, t:t + 1] = p @ vn[:, :, lo:hi]
+    n = np.maximum(np.sqrt(np.sum(h * h, axis=-1, keepdims=True)), eps)
+    return np.transpose(np.tanh(n) / n * h, (0, 2, 1, 3))
+
+
+def decode_row(q_new, kcache, vcache, cache_len, r, w, eps=EPS):
+    """Decode output (B,H,D) of the token at position cache_len-1 whose query
+    projection is q_new (B,H,D), against raw caches (B,T,H,D): row
+    cache_len-1 of forward() over the prefix (model.py:133 keeps only it)."""
+    q = np.asarray(q_new, dtype=np.float64)[:, None]
+    pos = cache_len - 1
+    y = _rows(q, np.asarray(kcache)[:, :cache_len], np.asarray(vcache)[:, :cache_len], r, w,
+              np.array([pos]), True, eps)
+    return y[:, 0]
+
+
+def tile_counts(q, k, r, w, causal=True, eps=EPS, tile=64, key_padding_mask=None, block=512):
+    """(|W|, |A|, active) over all heads: W = 64x64 tiles holding an in-window
+    pair; A = tiles holding an in-window, unmasked pair with 1 - r(1-s) > 0.
+    `active` is the (B,H,nqt,nkt) bool map of A."""
+    qn, kn = normalize(_heads(q), eps), normalize(_heads(k), eps)
+    B, H, Tq, D = qn.shape
+    Tk = kn.shape[2]
+    rr = np.asarray(r, dtype=np.float64).reshape(1, H, 1, 1)
+    nqt, nkt = -(-Tq // tile), -(-Tk // tile)
+    block = max(tile, block // tile * tile)
+    win = np.zeros((B, H, nqt, nkt), dtype=bool)
+    act = np.zeros((B, H, nqt, nkt), dtype=bool)
+    kpos = np.arange(Tk)
+    wv = np.asarray(w, dtype=np.float64).reshape(-1, 1, 1)
+    for i0, i1 in _blocks(Tq, block):
+        s = qn[:, :, i0:i1] @ np.swapaxes(kn, -1, -2)
+        rel = (kpos[None, :] - np.arange(i0, i1)[:, None]).astype(np.float64)[None]
+        inside = ((rel > -wv) & (rel <= 0)) if causal else (np.abs(rel) < wv)
+        live = (1.0 - rr * (1.0 - s) > 0) & inside[None]
+        if key_padding_mask is not None:
+            live = live & (~np.asarray(key_padding_mask, dtype=bool))[:, None, None, :]
+        inside = np.broadcast_to(inside[None], live.shape)
+        pq, pk = -(i1 - i0) % tile, nkt * tile - Tk
+        def tiles(x):
+            x = np.pad(x, ((0, 0), (0, 0), (0, pq), (0, pk)))
+            b_, h_, tq, tk = x.shape
+            return x.reshape(b_, h_, tq // tile, tile, tk // tile, tile).any(axis=(3, 5))
+        q0 = i0 // tile
+        win[:, :, q0:q0 + -(-(i1 - i0) // tile)] |= tiles(inside)
+        act[:, :, q0:q0 + -(-(i1 - i0) // tile)] |= tiles(live)
+    return int(win.sum()), int(act.sum()), act

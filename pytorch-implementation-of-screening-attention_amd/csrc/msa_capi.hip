@@ -1,0 +1,295 @@
+// C ABI of libmsa.so (declared in include/msa.h): argument validation on the
+// host, workspace carving, then stream-ordered kernel launches.  No device
+// memory is allocated here.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/msa.h"
+#include "msa_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return MSA_OK;
+}
+
+constexpr int kMaxT = 1 << 22;  // tile bitmap rows are kept to <= 2048 words
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Shared shape validation; fills g on success.
+int check_geometry(int B, int H, int Tq, int Tk, int D, int dtype, int causal, msa::Geometry* g) {
+  if (dtype != MSA_F32 && dtype != MSA_BF16) return fail(MSA_ERR_INVALID, "dtype must be MSA_F32 or MSA_BF16");
+  if (!(D == 16 || D == 32 || D == 64 || D == 128))
+    return fail(MSA_ERR_INVALID, "head_dim D=%d unsupported (16, 32, 64 or 128)", D);
+  if (B < 0 || H <= 0 || Tq < 0 || Tk < 0) return fail(MSA_ERR_INVALID, "negative or zero size");
+  if (Tq > kMaxT || Tk > kMaxT) return fail(MSA_ERR_INVALID, "sequence length above %d", kMaxT);
+  if ((int64_t)B * H > 65535) return fail(MSA_ERR_INVALID, "B*H=%lld above 65535", (long long)B * H);
+  g->B = B; g->H = H; g->Tq = Tq; g->Tk = Tk; g->D = D; g->DP = msa::padded_dim(D);
+  g->dtype = dtype; g->causal = causal ? 1 : 0;
+  g->nqt = msa::ntiles(Tq); g->nkt = msa::ntiles(Tk);
+  g->nkt_words = (g->nkt + 31) / 32;
+  g->Tq_pad = (int64_t)g->nqt * 64; g->Tk_pad = (int64_t)g->nkt * 64;
+  g->esize = dtype == MSA_BF16 ? 2 : 4;
+  return MSA_OK;
+}
+
+int check_tensor(const char* name, const void* p, int64_t sb, int64_t st, int64_t sh, int dtype) {
+  if (p == nullptr) return fail(MSA_ERR_INVALID, "%s is null", name);
+  if (!aligned16(p)) return fail(MSA_ERR_INVALID, "%s is not 16-byte aligned", name);
+  const int64_t m = dtype == MSA_BF16 ? 8 : 4;
+  if (sb < 0 || st < 0 || sh < 0 || sb % m || st % m || sh % m)
+    return fail(MSA_ERR_INVALID, "%s strides (%lld,%lld,%lld) must be non-negative multiples of %lld elements", name,
+                (long long)sb, (long long)st, (long long)sh, (long long)m);
+  return MSA_OK;
+}
+
+int check_out(const char* name, const void* p) {
+  if (p == nullptr) return fail(MSA_ERR_INVALID, "%s is null", name);
+  if (!aligned16(p)) return fail(MSA_ERR_INVALID, "%s is not 16-byte aligned", name);
+  return MSA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MSA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+struct TimerState {
+  std::mutex mu;
+  int kernel = 0;
+  int next = 0;
+  std::vector<hipEvent_t> start, stop;
+};
+TimerState& timer() {
+  static TimerState t;
+  return t;
+}
+
+}  // namespace
+
+namespace msa {
+void timer_begin(int kernel, hipStream_t s) {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  if (t.kernel == kernel && t.next < (int)t.start.size()) (void)hipEventRecord(t.start[t.next], s);
+}
+void timer_end(int kernel, hipStream_t s) {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  if (t.kernel == kernel && t.next < (int)t.stop.size()) (void)hipEventRecord(t.stop[t.next++], s);
+}
+}  // namespace msa
+
+extern "C" {
+
+int msa_timer_arm(int kernel, int n) {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  for (hipEvent_t e : t.start) (void)hipEventDestroy(e);
+  for (hipEvent_t e : t.stop) (void)hipEventDestroy(e);
+  t.start.clear();
+  t.stop.clear();
+  t.kernel = 0;
+  t.next = 0;
+  if (kernel == 0 || n <= 0) return ok();
+  if (kernel < MSA_K_PREP_KV || kernel > MSA_K_DECODE) return fail(MSA_ERR_INVALID, "unknown kernel id %d", kernel);
+  for (int i = 0; i < n; ++i) {
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
+      return fail(MSA_ERR_HIP, "hipEventCreate failed");
+    t.start.push_back(a);
+    t.stop.push_back(b);
+  }
+  t.kernel = kernel;
+  return ok();
+}
+
+int msa_timer_read(float* ms, int n) {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> g(t.mu);
+  int cnt = t.next < n ? t.next : n;
+  for (int i = 0; i < cnt; ++i) {
+    if (hipEventSynchronize(t.stop[i]) != hipSuccess) return -1;
+    if (hipEventElapsedTime(&ms[i], t.start[i], t.stop[i]) != hipSuccess) return -1;
+  }
+  return cnt;
+}
+
+
+int msa_version(void) { return (0 << 16) | (1 << 8) | 0; }
+
+const char* msa_last_error(void) { return g_last_error.c_str(); }
+
+size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype, int need_bwd) {
+  msa::Geometry g;
+  if (check_geometry(B, H, Tq, Tk, D, dtype, 1, &g) != MSA_OK) return 0;
+  return msa::fwd_ws_bytes(g, need_bwd);
+}
+
+size_t msa_tile_bits_words(int B, int H, int Tq, int Tk) {
+  if (B < 0 || H <= 0 || Tq < 0 || Tk < 0) return 0;
+  const int64_t nqt = msa::ntiles(Tq), nkt = msa::ntiles(Tk);
+  return (size_t)((int64_t)B * H * nqt * ((nkt + 31) / 32));
+}
+
+size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype) {
+  msa::Geometry g;
+  if (check_geometry(B, H, Tq, Tk, D, dtype, 1, &g) != MSA_OK) return 0;
+  return msa::bwd_ws_bytes(g);
+}
+
+int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_st,
+            int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int Tq, int Tk,
+            int D, int dtype, const float* r, const float* w, const uint8_t* key_padding_mask, int causal, float eps,
+            void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words, void* workspace,
+            size_t workspace_bytes, int need_bwd, void* stream) {
+  msa::Geometry g;
+  int rc = check_geometry(B, H, Tq, Tk, D, dtype, causal, &g);
+  if (rc != MSA_OK) return rc;
+  if (!(eps > 0.0f)) return fail(MSA_ERR_INVALID, "eps must be positive");
+  if (B == 0 || Tq == 0) return ok();
+  if ((rc = check_tensor("q", q, q_sb, q_st, q_sh, dtype)) != MSA_OK) return rc;
+  if (Tk > 0) {
+    if ((rc = check_tensor("k", k, k_sb, k_st, k_sh, dtype)) != MSA_OK) return rc;
+    if ((rc = check_tensor("v", v, v_sb, v_st, v_sh, dtype)) != MSA_OK) return rc;
+  }
+  if (r == nullptr || w == nullptr) return fail(MSA_ERR_INVALID, "r and w must be device arrays of H floats");
+  if ((rc = check_out("y", y)) != MSA_OK) return rc;
+  if (hnorm == nullptr) return fail(MSA_ERR_INVALID, "hnorm is null");
+  if (tile_bits == nullptr) return fail(MSA_ERR_INVALID, "tile_bits is null");
+  if (tile_bits_words < msa_tile_bits_words(B, H, Tq, Tk))
+    return fail(MSA_ERR_WORKSPACE, "tile_bits holds %zu words, %zu needed", tile_bits_words,
+                msa_tile_bits_words(B, H, Tq, Tk));
+  const size_t need = msa::fwd_ws_bytes(g, need_bwd);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+    return fail(MSA_ERR_WORKSPACE, "forward workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  if (need > 0 && !aligned16(workspace)) return fail(MSA_ERR_INVALID, "workspace is not 16-byte aligned");
+
+  msa::FwdCall c;
+  c.g = g;
+  c.q = q; c.qs = {q_sb, q_st, q_sh};
+  c.k = k; c.ks = {k_sb, k_st, k_sh};
+  c.v = v; c.vs = {v_sb, v_st, v_sh};
+  c.r = r; c.w = w; c.kpm = key_padding_mask; c.eps = eps;
+  c.y = y; c.hnorm = hnorm; c.bits = tile_bits;
+  c.ws = msa::fwd_ws_carve(g, workspace, need_bwd);
+  c.need_bwd = need_bwd;
+  c.stream = (hipStream_t)stream;
+  return hip_status(msa::launch_fwd(c), "msa_fwd launch");
+}
+
+int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_st,
+            int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int Tq, int Tk,
+            int D, int dtype, const float* r, const float* w, int causal, float eps, const void* y,
+            const float* hnorm, const void* dy, const uint32_t* tile_bits, size_t tile_bits_words,
+            const void* fwd_workspace, size_t fwd_workspace_bytes, void* dq, void* dk, void* dv, float* dr,
+            float* dw, void* workspace, size_t workspace_bytes, void* stream) {
+  msa::Geometry g;
+  int rc = check_geometry(B, H, Tq, Tk, D, dtype, causal, &g);
+  if (rc != MSA_OK) return rc;
+  if (!(eps > 0.0f)) return fail(MSA_ERR_INVALID, "eps must be positive");
+  if (dr == nullptr || dw == nullptr) return fail(MSA_ERR_INVALID, "dr and dw must be device arrays of H floats");
+  if (B == 0 || Tq == 0 || Tk == 0)
+    return fail(MSA_ERR_INVALID, "msa_bwd needs B, Tq, Tk > 0 (the caller zero-fills empty gradients)");
+  if ((rc = check_tensor("q", q, q_sb, q_st, q_sh, dtype)) != MSA_OK) return rc;
+  if ((rc = check_tensor("k", k, k_sb, k_st, k_sh, dtype)) != MSA_OK) return rc;
+  if ((rc = check_tensor("v", v, v_sb, v_st, v_sh, dtype)) != MSA_OK) return rc;
+  if (r == nullptr || w == nullptr) return fail(MSA_ERR_INVALID, "r and w must be device arrays of H floats");
+  if ((rc = check_out("y", y)) != MSA_OK) return rc;
+  if ((rc = check_out("dy", dy)) != MSA_OK) return rc;
+  if ((rc = check_out("dq", dq)) != MSA_OK) return rc;
+  if ((rc = check_out("dk", dk)) != MSA_OK) return rc;
+  if ((rc = check_out("dv", dv)) != MSA_OK) return rc;
+  if (hnorm == nullptr || tile_bits == nullptr) return fail(MSA_ERR_INVALID, "hnorm / tile_bits is null");
+  if (tile_bits_words < msa_tile_bits_words(B, H, Tq, Tk))
+    return fail(MSA_ERR_WORKSPACE, "tile_bits holds %zu words, %zu needed", tile_bits_words,
+                msa_tile_bits_words(B, H, Tq, Tk));
+  const size_t fneed = msa::fwd_ws_bytes(g, 1);
+  if (fwd_workspace == nullptr || fwd_workspace_bytes < fneed)
+    return fail(MSA_ERR_WORKSPACE, "forward workspace holds %zu bytes, %zu needed (msa_fwd with need_bwd=1)",
+                fwd_workspace_bytes, fneed);
+  const size_t need = msa::bwd_ws_bytes(g);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(MSA_ERR_WORKSPACE, "backward workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  if (!aligned16(workspace) || !aligned16(fwd_workspace))
+    return fail(MSA_ERR_INVALID, "workspaces must be 16-byte aligned");
+
+  msa::BwdCall c;
+  c.g = g;
+  c.q = q; c.qs = {q_sb, q_st, q_sh};
+  c.k = k; c.ks = {k_sb, k_st, k_sh};
+  c.v = v; c.vs = {v_sb, v_st, v_sh};
+  c.r = r; c.w = w; c.eps = eps;
+  c.y = y; c.hnorm = hnorm; c.dy = dy; c.bits = tile_bits;
+  c.fws = msa::fwd_ws_carve(g, const_cast<void*>(fwd_workspace), 1);
+  c.bws = msa::bwd_ws_carve(g, workspace);
+  c.dq = dq; c.dk = dk; c.dv = dv; c.dr = dr; c.dw = dw;
+  c.stream = (hipStream_t)stream;
+  return hip_status(msa::launch_bwd(c), "msa_bwd launch");
+}
+
+size_t msa_decode_workspace_bytes(int B, int H, int D, int max_len) {
+  if (B <= 0 || H <= 0 || max_len <= 0 || !(D == 16 || D == 32 || D == 64 || D == 128)) return 0;
+  return (size_t)B * H * msa::decode_max_chunks(max_len) * D * sizeof(float);
+}
+
+int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
+               int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int D,
+               int dtype, int cache_len, int cache_cap, const float* r, const float* w, float eps, void* y,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  msa::Geometry g;
+  int rc = check_geometry(B, H, 1, cache_len, D, dtype, 1, &g);
+  if (rc != MSA_OK) return rc;
+  if (B == 0) return ok();
+  if (cache_len <= 0) return fail(MSA_ERR_INVALID, "cache_len must be >= 1 (the new token is in the cache)");
+  if (cache_len > cache_cap)
+    return fail(MSA_ERR_INVALID, "cache_len %d exceeds the cache capacity %d", cache_len, cache_cap);
+  if (!(eps > 0.0f)) return fail(MSA_ERR_INVALID, "eps must be positive");
+  if ((rc = check_tensor("q", q, q_sb, 0, q_sh, dtype)) != MSA_OK) return rc;
+  if ((rc = check_tensor("kcache", kcache, k_sb, k_st, k_sh, dtype)) != MSA_OK) return rc;
+  if ((rc = check_tensor("vcache", vcache, v_sb, v_st, v_sh, dtype)) != MSA_OK) return rc;
+  if (r == nullptr || w == nullptr) return fail(MSA_ERR_INVALID, "r and w must be device arrays of H floats");
+  if ((rc = check_out("y", y)) != MSA_OK) return rc;
+  const size_t need = msa_decode_workspace_bytes(B, H, D, cache_len);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(MSA_ERR_WORKSPACE, "decode workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  msa::DecodeCall c;
+  c.B = B; c.H = H; c.D = D; c.DP = g.DP; c.dtype = dtype; c.len = cache_len;
+  c.q = q; c.q_sb = q_sb; c.q_sh = q_sh;
+  c.kc = kcache; c.ks = {k_sb, k_st, k_sh};
+  c.vc = vcache; c.vs = {v_sb, v_st, v_sh};
+  c.r = r; c.w = w; c.eps = eps;
+  c.y = y; c.part = (float*)workspace;
+  c.nchunks = msa::decode_max_chunks(cache_len);
+  c.chunk = msa::decode_chunk_keys();
+  c.stream = (hipStream_t)stream;
+  return hip_status(msa::launch_decode(c), "msa_decode launch");
+}
+
+int msa_selftest_mfma(const float* a16, const float* b16, float* out16, const float* a2, const float* b2,
+                      float* out2, void* stream) {
+  if (!a16 || !b16 || !out16 || !a2 || !b2 || !out2) return fail(MSA_ERR_INVALID, "null pointer");
+  return hip_status(msa::launch_selftest(a16, b16, out16, a2, b2, out2, (hipStream_t)stream), "selftest launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,223 @@
+// Single-query decode against a KV cache (gfx950).
+//
+// The query at position pos = len-1 attends to keys j in (pos - w, pos]
+// (causal window, attention.py:111-118).  The window is split into chunks of
+// kChunk keys; each 256-thread block streams one chunk of raw K rows
+// (16-byte loads, D/VEC lanes per key), forms s = q^.k^ on the fly,
+// and reads a V row only when its alpha*m is non-zero.  Because screening has
+// no softmax normaliser (attention.py:192-193), chunk partials simply add; a
+// second kernel sums them in a fixed order and applies TanhNorm (norm.py:23-25).
+#include "msa_device.h"
+#include "msa_internal.h"
+
+namespace msa {
+
+constexpr int kChunk = 2048;
+constexpr int kDecUnroll = 4;
+
+struct DecArgs {
+  const void* q; int64_t q_sb, q_sh;
+  const void* kc; Strides3 ks;
+  const void* vc; Strides3 vs;
+  const float* r; const float* w;
+  float* part;  // [B*H][nchunks][D]
+  void* y;
+  int H, len, nchunks;
+  float eps;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
+  constexpr int VEC = 16 / (int)sizeof(T);  // elements per 16-byte load
+  constexpr int LPK = D / VEC;              // lanes per key row
+  constexpr int KPW = kWave / LPK;          // keys per wave per load
+  __shared__ float red[4][D];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const HeadParams hp = head_params(a.r, a.w, h);
+  const int64_t pos = a.len - 1;
+  int64_t lo = pos - hp.wc + 1;
+  if (lo < 0) lo = 0;
+  const int64_t n = pos - lo + 1;
+  const int64_t c0 = lo + (int64_t)blockIdx.x * kChunk;
+  const int sub = lane % LPK, kl = lane / LPK;
+  const int d0 = sub * VEC;
+
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+
+  if ((int64_t)blockIdx.x * kChunk < n) {
+    // query chunk and its norm (each LPK-lane group covers the whole row)
+    float qv[VEC];
+    {
+      const T* qp = (const T*)a.q + b * a.q_sb + h * a.q_sh + d0;
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4) {
+        f32x4 x = load4(qp + e);
+        qv[e] = x[0]; qv[e + 1] = x[1]; qv[e + 2] = x[2]; qv[e + 3] = x[3];
+        ss += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+      }
+#pragma unroll
+      for (int o = 1; o < LPK; o <<= 1) ss += __shfl_xor(ss, o);
+      const float iq = 1.0f / fmaxf(sqrtf(ss), a.eps);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qv[e] *= iq;
+    }
+    const int64_t cend = c0 + kChunk < pos + 1 ? c0 + kChunk : pos + 1;
+    const T* kb = (const T*)a.kc + b * a.ks.sb + h * a.ks.sh + d0;
+    const T* vb = (const T*)a.vc + b * a.vs.sb + h * a.vs.sh + d0;
+    for (int64_t base = c0 + (int64_t)wave * KPW * kDecUnroll; base < cend; base += 4 * KPW * kDecUnroll) {
+      float kv[kDecUnroll][VEC];
+      bool ok[kDecUnroll];
+#pragma unroll
+      for (int u = 0; u < kDecUnroll; ++u) {
+        const int64_t j = base + u * KPW + kl;
+        ok[u] = j < cend;
+        const T* kp = kb + (ok[u] ? j : c0) * a.ks.st;
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4) {
+          f32x4 x = load4(kp + e);
+          kv[u][e] = x[0]; kv[u][e + 1] = x[1]; kv[u][e + 2] = x[2]; kv[u][e + 3] = x[3];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kDecUnroll; ++u) {
+        float dot = 0.0f, ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) { dot += qv[e] * kv[u][e]; ss += kv[u][e] * kv[u][e]; }
+#pragma unroll
+        for (int o = 1; o < LPK; o <<= 1) { dot += __shfl_xor(dot, o); ss += __shfl_xor(ss, o); }
+        const float s = dot * (1.0f / fmaxf(sqrtf(ss), a.eps));
+        const float av = trim(s, hp.r);
+        const int64_t j = base + u * KPW + kl;
+        if (ok[u] && av > 0.0f) {
+          const float m = softmask(pos - j, hp.iw);
+          const T* vp = vb + j * a.vs.st;
+          float vv[VEC], vs2 = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; e += 4) {
+            f32x4 x = load4(vp + e);
+            vv[e] = x[0]; vv[e + 1] = x[1]; vv[e + 2] = x[2]; vv[e + 3] = x[3];
+            vs2 += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+          }
+          // every lane of the key's group takes this branch together
+#pragma unroll
+          for (int o = 1; o < LPK; o <<= 1) vs2 += __shfl_xor(vs2, o);
+          const float coef = av * av * m / fmaxf(sqrtf(vs2), a.eps);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] += coef * vv[e];
+        }
+      }
+    }
+  }
+  // reduce over the key groups of the wave, then over the 4 waves
+#pragma unroll
+  for (int o = LPK; o < kWave; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], o);
+  if (kl == 0)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[wave][d0 + e] = acc[e];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    a.part[((int64_t)bh * a.nchunks + blockIdx.x) * D + d] = red[0][d] + red[1][d] + red[2][d] + red[3][d];
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(128) void decode_reduce_kernel(DecArgs a) {
+  __shared__ float red[128];
+  const int bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const HeadParams hp = head_params(a.r, a.w, bh % a.H);
+  const int64_t pos = a.len - 1;
+  int64_t lo = pos - hp.wc + 1;
+  if (lo < 0) lo = 0;
+  const int used = (int)((pos - lo + 1 + kChunk - 1) / kChunk);
+  float x = 0.0f;
+  if (d < D)
+    for (int c = 0; c < used; ++c) x += a.part[((int64_t)bh * a.nchunks + c) * D + d];
+  red[d] = x * x;
+  __syncthreads();
+  for (int s = 64; s > 0; s >>= 1) {
+    if (d < s) red[d] += red[d + s];
+    __syncthreads();
+  }
+  const float nc = fmaxf(sqrtf(red[0]), a.eps);
+  const float f = tanhf(nc) / nc;
+  if (d < D) ((T*)a.y)[(int64_t)bh * D + d] = from_f<T>(f * x);
+}
+
+int decode_chunk_keys() { return kChunk; }
+int decode_max_chunks(int max_len) { return (max_len + kChunk - 1) / kChunk; }
+
+template <typename T, int D>
+static hipError_t launch_decode_t(const DecodeCall& c) {
+  DecArgs a;
+  a.q = c.q; a.q_sb = c.q_sb; a.q_sh = c.q_sh;
+  a.kc = c.kc; a.ks = c.ks; a.vc = c.vc; a.vs = c.vs;
+  a.r = c.r; a.w = c.w; a.part = c.part; a.y = c.y;
+  a.H = c.H; a.len = c.len; a.nchunks = c.nchunks; a.eps = c.eps;
+  timer_begin(7, c.stream);
+  hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3((unsigned)c.nchunks, (unsigned)(c.B * c.H)), dim3(256), 0,
+                     c.stream, a);
+  timer_end(7, c.stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((decode_reduce_kernel<T, D>), dim3((unsigned)(c.B * c.H)), dim3(128), 0, c.stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode(const DecodeCall& c) {
+  if (c.dtype == 1) {
+    switch (c.D) {
+      case 16: return launch_decode_t<bf16, 16>(c);
+      case 32: return launch_decode_t<bf16, 32>(c);
+      case 64: return launch_decode_t<bf16, 64>(c);
+      default: return launch_decode_t<bf16, 128>(c);
+    }
+  }
+  switch (c.D) {
+    case 16: return launch_decode_t<float, 16>(c);
+    case 32: return launch_decode_t<float, 32>(c);
+    case 64: return launch_decode_t<float, 64>(c);
+    default: return launch_decode_t<float, 128>(c);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA layout self-test: one wave computes a 32x32 product with each operand
+// form, loading operands and storing the result with the lane maps the
+// kernels use.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void selftest_kernel(const float* a16, const float* b16, float* out16,
+                                                      const float* a2, const float* b2, float* out2) {
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  bf16x8 fa, fb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    fa[e] = (bf16)a16[l32 * 16 + 8 * half + e];      // A[m=l32][k]
+    fb[e] = (bf16)b16[(8 * half + e) * 32 + l32];    // B[k][n=l32]
+  }
+  f32x16 c = {};
+  c = Mma<bf16>::mma(fa, fb, c);
+  f32x16 c2 = {};
+  c2 = Mma<float>::mma(a2[l32 * 2 + half], b2[half * 32 + l32], c2);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r / 4) + 4 * half + (r % 4);
+    out16[row * 32 + l32] = c[r];
+    out2[row * 32 + l32] = c2[r];
+  }
+}
+
+hipError_t launch_selftest(const float* a16, const float* b16, float* out16, const float* a2, const float* b2,
+                           float* out2, hipStream_t stream) {
+  hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, a16, b16, out16, a2, b2, out2);
+  return hipGetLastError();
+}
+
+}  // namespace msa

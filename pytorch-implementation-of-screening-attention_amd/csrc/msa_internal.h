@@ -1,0 +1,95 @@
+// Host-side internal interface between the C ABI (msa_capi.hip) and the
+// kernel translation units.  Everything here is validated before use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace msa {
+
+// Padded head dimension the kernels are instantiated for.
+inline int padded_dim(int D) { return D <= 32 ? 32 : (D <= 64 ? 64 : 128); }
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+inline int ntiles(int64_t T) { return (int)((T + 63) / 64); }
+
+struct Geometry {
+  int B, H, Tq, Tk, D, DP, dtype, causal;
+  int nqt, nkt, nkt_words;
+  int64_t Tq_pad, Tk_pad;
+  size_t esize;  // bytes per element of dtype
+};
+
+struct Strides3 { int64_t sb, st, sh; };
+
+// Forward workspace (normalised key/value copies), each (B*H) x ... :
+//   khat  [bh][Tk_pad][DP]   row layout           (always)
+//   vhatT [bh][DP][Tk_pad]   transposed           (always)
+//   khatT [bh][DP][Tk_pad]   transposed           (need_bwd)
+//   vhat  [bh][Tk_pad][DP]   row layout           (need_bwd)
+struct FwdWs {
+  void* khat; void* vhatT; void* khatT; void* vhat;
+};
+size_t fwd_ws_bytes(const Geometry& g, int need_bwd);
+FwdWs fwd_ws_carve(const Geometry& g, void* base, int need_bwd);
+
+// Backward workspace:
+//   qhat  [bh][Tq_pad][DP], qhatT [bh][DP][Tq_pad]
+//   dh    [bh][Tq_pad][DP], dhT   [bh][DP][Tq_pad]
+//   part  [2][bh][nkt] fp32 per-wave partial sums of dr and dw
+struct BwdWs {
+  void* qhat; void* qhatT; void* dh; void* dhT; float* part;
+};
+size_t bwd_ws_bytes(const Geometry& g);
+BwdWs bwd_ws_carve(const Geometry& g, void* base);
+
+struct FwdCall {
+  Geometry g;
+  const void* q; Strides3 qs;
+  const void* k; Strides3 ks;
+  const void* v; Strides3 vs;
+  const float* r; const float* w; const uint8_t* kpm;
+  float eps;
+  void* y; float* hnorm; uint32_t* bits;
+  FwdWs ws; int need_bwd;
+  hipStream_t stream;
+};
+hipError_t launch_fwd(const FwdCall& c);
+
+struct BwdCall {
+  Geometry g;
+  const void* q; Strides3 qs;
+  const void* k; Strides3 ks;
+  const void* v; Strides3 vs;
+  const float* r; const float* w;
+  float eps;
+  const void* y; const float* hnorm; const void* dy;
+  const uint32_t* bits;
+  FwdWs fws; BwdWs bws;
+  void* dq; void* dk; void* dv; float* dr; float* dw;
+  hipStream_t stream;
+};
+hipError_t launch_bwd(const BwdCall& c);
+
+struct DecodeCall {
+  int B, H, D, DP, dtype, len;
+  const void* q; int64_t q_sb, q_sh;
+  const void* kc; Strides3 ks;
+  const void* vc; Strides3 vs;
+  const float* r; const float* w; float eps;
+  void* y; float* part; int nchunks; int chunk;
+  hipStream_t stream;
+};
+int decode_chunk_keys();
+int decode_max_chunks(int max_len);
+hipError_t launch_decode(const DecodeCall& c);
+
+// Optional event pairs around one kernel's launches (msa_timer_arm).
+void timer_begin(int kernel, hipStream_t s);
+void timer_end(int kernel, hipStream_t s);
+
+hipError_t launch_selftest(const float* a16, const float* b16, float* out16,
+                           const float* a2, const float* b2, float* out2,
+                           hipStream_t stream);
+
+}  // namespace msa

@@ -1,0 +1,129 @@
+"""MultiscreenLM: causal language model built from Multiscreen blocks.
+
+Reference: multiscreen/model.py:12-141.  Same constructor, submodule names
+(token_emb, pos_emb, emb_dropout, blocks, norm, lm_head), tied weights,
+initialisation (_init_weights, model.py:64-69), forward() contract (logits and
+an un-shifted cross-entropy with ignore_index=-100, model.py:101-106) and
+generate() signature and sampling (temperature, optional top-k, multinomial,
+model.py:111-141).
+
+generate() differs only in cost: instead of re-running forward() over the
+whole prefix for every new token, it prefills a per-layer KV cache once and
+then runs one single-query decode step per token (the HIP decode kernel on
+GPU), which computes the same last-position logits.
+"""
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import KVCache
+from .layers import MultiscreenBlock
+
+
+class MultiscreenLM(nn.Module):
+    def __init__(self, vocab_size: int, d_model: int = 512, num_heads: int = 8, num_layers: int = 6,
+                 ffn_dim: int | None = None, max_seq_len: int = 2048, dropout: float = 0.0,
+                 tie_weights: bool = True):
+        super().__init__()
+        self.d_model = d_model
+        self.token_emb = nn.Embedding(vocab_size, d_model)
+        self.pos_emb = nn.Embedding(max_seq_len, d_model)
+        self.emb_dropout = nn.Dropout(dropout)
+        self.blocks = nn.ModuleList([
+            MultiscreenBlock(d_model=d_model, num_heads=num_heads, ffn_dim=ffn_dim, dropout=dropout,
+                             causal=True)
+            for _ in range(num_layers)
+        ])
+        self.norm = nn.RMSNorm(d_model)
+        self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
+        if tie_weights:
+            self.lm_head.weight = self.token_emb.weight
+        self._init_weights()
+
+    def _init_weights(self):
+        nn.init.normal_(self.token_emb.weight, std=0.02)
+        nn.init.normal_(self.pos_emb.weight, std=0.02)
+        for module in self.modules():
+            if isinstance(module, nn.Linear):
+                nn.init.normal_(module.weight, std=0.02)
+
+    def embed(self, input_ids: torch.Tensor, start: int = 0) -> torch.Tensor:
+        T = input_ids.shape[1]
+        positions = torch.arange(start, start + T, device=input_ids.device).unsqueeze(0)
+        return self.emb_dropout(self.token_emb(input_ids) + self.pos_emb(positions))
+
+    def forward(self, input_ids: torch.Tensor, key_padding_mask: torch.Tensor | None = None,
+                labels: torch.Tensor | None = None) -> dict[str, torch.Tensor]:
+        """
+        Args:
+            input_ids:        (B, T) integer token ids.
+            key_padding_mask: (B, T) bool -- True = padding position.
+            labels:           (B, T) token ids; -100 is ignored.
+        Returns:
+            {'logits': (B, T, vocab)} plus 'loss' when labels are given.
+        """
+        x = self.embed(input_ids)
+        for block in self.blocks:
+            x = block(x, key_padding_mask=key_padding_mask)
+        logits = self.lm_head(self.norm(x))
+        result = {"logits": logits}
+        if labels is not None:
+            result["loss"] = F.cross_entropy(logits.view(-1, logits.size(-1)), labels.view(-1),
+                                             ignore_index=-100)
+        return result
+
+    def new_cache(self, batch: int, capacity: int, dtype: torch.dtype, device) -> list:
+        attn = self.blocks[0].attn
+        return [KVCache(batch, capacity, attn.num_heads, attn.head_dim, dtype, device)
+                for _ in self.blocks]
+
+    def _head(self, x: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(self.norm(x))
+
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor, caches: list) -> torch.Tensor:
+        """Runs the prompt once, filling `caches`; returns last-position logits (B, vocab)."""
+        x = self.embed(input_ids)
+        for block, cache in zip(self.blocks, caches):
+            x = block.prefill(x, cache)
+        return self._head(x[:, -1:])[:, 0]
+
+    @torch.no_grad()
+    def decode_step(self, token: torch.Tensor, caches: list, pos: int) -> torch.Tensor:
+        """token (B,1) at position `pos`; returns its logits (B, vocab)."""
+        x = self.embed(token, start=pos)
+        for block, cache in zip(self.blocks, caches):
+            x = block.decode(x, cache, pos)
+        return self._head(x)[:, 0]
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100, temperature: float = 1.0,
+                 top_k: int | None = None) -> torch.Tensor:
+        """Temperature / top-k sampling (top_k=1 is greedy).
+
+        Returns (B, T + max_new_tokens) token ids.
+        """
+        self.eval()
+        B, T = input_ids.shape
+        if max_new_tokens <= 0:
+            return input_ids
+        dtype = self.blocks[0].attn.q_proj.weight.dtype
+        if input_ids.is_cuda and torch.is_autocast_enabled("cuda"):
+            dtype = torch.get_autocast_dtype("cuda")
+        caches = self.new_cache(B, T + max_new_tokens, dtype, input_ids.device)
+        logits = self.prefill(input_ids, caches)
+        out = [input_ids]
+        pos = T
+        for step in range(max_new_tokens):
+            logits = logits / temperature
+            if top_k is not None:
+                values, _ = torch.topk(logits, top_k)
+                logits[logits < values[:, -1:]] = float("-inf")
+            probs = F.softmax(logits, dim=-1)
+            next_token = torch.multinomial(probs, num_samples=1)
+            out.append(next_token)
+            if step + 1 < max_new_tokens:
+                logits = self.decode_step(next_token, caches, pos)
+                pos += 1
+        return torch.cat(out, dim=1)

@@ -1,0 +1,37 @@
+"""Test configuration: import paths and the `gpu` marker.
+
+`gpu` tests need an MI355X (gfx950) and call the HIP kernels through the C ABI
+of libmsa.so; they are skipped where no GPU is visible.  Everything else runs
+on the CPU.
+"""
+
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "pytorch-implementation-of-screening-attention_amd")
+for p in (PKG, os.path.join(ROOT, "oracle"), os.path.dirname(os.path.abspath(__file__))):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU and the built libmsa.so")
+
+
+def _have_gpu():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def pytest_collection_modifyitems(config, items):
+    if any("gpu" in item.keywords for item in items) and not _have_gpu():
+        skip = pytest.mark.skip(reason="no GPU visible")
+        for item in items:
+            if "gpu" in item.keywords:
+                item.add_marker(skip)
