@@ -40,6 +40,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--calib-copy", action="store_true",
+                   help="end with a plain 256 MiB device copy (rocprofv3 --pmc byte-counter calibration)")
     return p.parse_args()
 
 
@@ -249,6 +251,13 @@ def main():
         out["decode"] = decode_bench(L, ops, torch)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, H, D, r, w, args.seed)
+    if args.calib_copy:
+        src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        out["calib_copy_bytes"] = src.numel() * 2
     print(json.dumps(out), flush=True)
 
 
