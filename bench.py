@@ -171,8 +171,8 @@ def main():
     wg = torch.tensor(w, device=dev)
 
     def step():
-        y, hnorm, bits, ws = ops.fwd_raw(q, k, v, rg, wg, True, 1e-8, None, need_bwd=True)
-        grads = ops.bwd_raw(q, k, v, rg, wg, True, 1e-8, y, hnorm, bits, ws, dy)
+        y, hnorm, bits = ops.fwd_raw(q, k, v, rg, wg, True, 1e-8, None)
+        grads = ops.bwd_raw(q, k, v, rg, wg, True, 1e-8, y, hnorm, bits, dy)
         return bits
 
     for _ in range(args.warmup):
@@ -201,8 +201,8 @@ def main():
 
     # per-kernel breakdown (outside the timed region)
     breakdown = {"fwd_kernel": fwd_ms}
-    for kid, name in ((1, "prep_kv_kernel"), (3, "bwd_prep_kernel"), (4, "dkdv_kernel"),
-                      (5, "dq_kernel"), (6, "rw_reduce_kernel")):
+    for kid, name in ((1, "prep_k_kernel"), (4, "dkdv_kernel"), (5, "dq_kernel"),
+                      (6, "rw_reduce_kernel")):
         breakdown[name] = kernel_times(L, kid, step, 5)[0]
     torch.cuda.synchronize()
 

@@ -58,18 +58,19 @@ int msa_version(void);
 /* Thread-local text of the last error raised on this thread ("" if none). */
 const char* msa_last_error(void);
 
-/* Bytes of forward workspace: normalised K^/V^ copies in the layouts the
- * kernels read.  need_bwd=1 adds the copies the backward reads; the same
- * workspace must then be handed unchanged to msa_bwd. */
-size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype,
-                               int need_bwd);
+/* Bytes of forward workspace: scratch for one unit-normalised copy of K (key
+ * padding applied, rows padded to a multiple of 64, head_dim padded to
+ * 32/64/128) that the forward stages through LDS.  Not needed afterwards. */
+size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
 /* Number of uint32 words of the active-tile bitmap: one bit per
  * (b, h, 64-query tile, 64-key tile), set iff some in-window, unmasked pair of
- * the tile has alpha > 0. */
+ * the tile has alpha > 0.  Row (b, h, query tile) holds ceil(nkt/32) words,
+ * bit kt%32 of word kt/32. */
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);
 
-/* Bytes of backward workspace. */
+/* Bytes of backward workspace: one (dr, dw) partial per (b, h, 64-key tile),
+ * summed in a fixed order. */
 size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
 /*
@@ -91,8 +92,7 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
             const float* r, const float* w, const uint8_t* key_padding_mask,
             int causal, float eps,
             void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words,
-            void* workspace, size_t workspace_bytes, int need_bwd,
-            void* stream);
+            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Fused backward.  Replaces _ScreeningFunc.backward / screening_attention_bwd
@@ -101,18 +101,19 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
  * reference fused path, which returns None for them (attention_triton.py:44)
  * -- produces the per-head gradients dr, dw (H,) that attention.py's autograd
  * delivers to s_r / s_v through r = exp(s_r)+1, w = exp(s_v)+1.
+ * Inputs: the forward's q, k, v, r, w, key_padding_mask, causal, eps and its
+ * outputs y, hnorm, tile_bits; dy (B,Tq,H,D) contiguous.
  * dq (B,Tq,H,D), dk, dv (B,Tk,H,D) are written in full (zeros where no
  * active pair reaches a row).  Deterministic: no atomics.
- * fwd_workspace is the one filled by msa_fwd with need_bwd=1.
  */
 int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
             const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
             const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
             int B, int H, int Tq, int Tk, int D, int dtype,
-            const float* r, const float* w, int causal, float eps,
+            const float* r, const float* w, const uint8_t* key_padding_mask,
+            int causal, float eps,
             const void* y, const float* hnorm, const void* dy,
             const uint32_t* tile_bits, size_t tile_bits_words,
-            const void* fwd_workspace, size_t fwd_workspace_bytes,
             void* dq, void* dk, void* dv, float* dr, float* dw,
             void* workspace, size_t workspace_bytes, void* stream);
 
@@ -145,7 +146,7 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
  * recorded.  msa_timer_arm(0, 0) disarms.  Process-wide; not for concurrent
  * use from several threads. */
 enum msa_kernel_id {
-  MSA_K_PREP_KV = 1, MSA_K_FWD = 2, MSA_K_BWD_PREP = 3, MSA_K_DKDV = 4,
+  MSA_K_PREP_K = 1, MSA_K_FWD = 2, /* 3: unused */ MSA_K_DKDV = 4,
   MSA_K_DQ = 5, MSA_K_RW_REDUCE = 6, MSA_K_DECODE = 7
 };
 int msa_timer_arm(int kernel, int n);

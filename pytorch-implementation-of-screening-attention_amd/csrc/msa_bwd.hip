@@ -11,13 +11,19 @@
 //   dq^_i  = sum_j ds_ij k^_j,   dk^_j = sum_i ds_ij q^_i
 //   dr     = -sum 2 a (1-s) m dP,  dw = sum a^2 dP dm/dw
 //   dx     = (dx^ - x^ (x^.dx^)) / |x|   (|x| > eps),  dx^/eps otherwise
-// Only tiles the forward marked live in its bitmap are revisited.
+// Only the tiles the forward marked live in its bitmap are revisited; each
+// wave turns its bitmap row/column into a 64-bit ballot mask and walks the set
+// bits.  MFMA operands are the raw q, k, v values (exact in bf16) and the
+// 1/|x| factors are applied in fp32 to the products, so no normalised copy is
+// rounded; dh is formed on the fly from y, dy and |h|.  Operands needed
+// transposed go through a wave-private LDS tile, per-row scale factors
+// through a small LDS vector.  Key padding (attention.py:185-188) enters as a
+// zero 1/|k|, which gives s = 0 and so alpha = 0 for those keys.
 //
-//   bwd_prep_kernel : per query row: q^ (row + transposed copies) and dh.
-//   dkdv_kernel     : wave per 64-key tile, loops over live query tiles;
-//                     accumulates dv^, dk^ in MFMA registers, writes dk, dv
-//                     and one (dr, dw) partial per wave.
-//   dq_kernel       : wave per 64-query tile, loops over live key tiles.
+//   dkdv_kernel     : wave per 64-key tile; accumulates dv^, dk^ in MFMA
+//                     registers over its live query tiles, writes dk, dv and
+//                     one (dr, dw) partial.
+//   dq_kernel       : wave per 64-query tile over its live key tiles.
 //   rw_reduce_kernel: fixed-order sum of the partials -> dr, dw.
 // No atomics anywhere, so every gradient is bitwise reproducible.
 #include "msa_device.h"
@@ -35,72 +41,15 @@ __device__ inline float tanhnorm_g(float n, float t) {
   return ((1.0f - t * t) / n - t / (n * n)) / n;
 }
 
-struct BwdPrepArgs {
-  const void* q; Strides3 qs;
-  const void* y; const void* dy; const float* hnorm;
-  void* qhat; void* qhatT; void* dh; void* dhT;
-  int H, Tq, D;
-  int64_t Tq_pad;
-  float eps;
-};
-
-// One thread per query row; grid (Tq_pad/64, B*H), block 64.
-template <typename T, int DP>
-__global__ __launch_bounds__(64) void bwd_prep_kernel(BwdPrepArgs a) {
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  const bool valid = i < a.Tq;
-  float x[DP];
-  {
-    const T* src = (const T*)a.q;
-    float ss = 0.0f;
-#pragma unroll
-    for (int d = 0; d < DP; d += 4) {
-      f32x4 v4 = {0.f, 0.f, 0.f, 0.f};
-      if (valid && d < a.D) v4 = load4(src + b * a.qs.sb + i * a.qs.st + h * a.qs.sh + d);
-      x[d] = v4[0]; x[d + 1] = v4[1]; x[d + 2] = v4[2]; x[d + 3] = v4[3];
-      ss += v4[0] * v4[0] + v4[1] * v4[1] + v4[2] * v4[2] + v4[3] * v4[3];
-    }
-    const float inv = valid ? 1.0f / fmaxf(sqrtf(ss), a.eps) : 0.0f;
-    T* row = (T*)a.qhat + ((int64_t)bh * a.Tq_pad + i) * DP;
-    T* col = (T*)a.qhatT + (int64_t)bh * DP * a.Tq_pad + i;
-#pragma unroll
-    for (int d = 0; d < DP; d += 4) store4(row + d, x[d] * inv, x[d + 1] * inv, x[d + 2] * inv, x[d + 3] * inv);
-#pragma unroll
-    for (int d = 0; d < DP; ++d) col[(int64_t)d * a.Tq_pad] = from_f<T>(x[d] * inv);
-  }
-  {
-    const T* yp = (const T*)a.y + (((int64_t)b * a.Tq + (valid ? i : 0)) * a.H + h) * a.D;
-    const T* gp = (const T*)a.dy + (((int64_t)b * a.Tq + (valid ? i : 0)) * a.H + h) * a.D;
-    float yv[DP];
-    float ydot = 0.0f;
-#pragma unroll
-    for (int d = 0; d < DP; d += 4) {
-      f32x4 y4 = {0.f, 0.f, 0.f, 0.f}, g4 = {0.f, 0.f, 0.f, 0.f};
-      if (valid && d < a.D) { y4 = load4(yp + d); g4 = load4(gp + d); }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { yv[d + e] = y4[e]; x[d + e] = g4[e]; ydot += y4[e] * g4[e]; }
-    }
-    const float n = valid ? a.hnorm[(int64_t)bh * a.Tq + i] : 0.0f;
-    // dh = F dy + G (h.dy) h with h = y/F  ->  dh = F dy + (G/F^2)(y.dy) y
-    float c1, c2;
-    if (n > a.eps) {
-      const float t = tanhf(n);
-      c1 = t / n;
-      c2 = tanhnorm_g(n, t) / (c1 * c1);
-    } else {
-      c1 = tanhf(a.eps) / a.eps;
-      c2 = 0.0f;
-    }
-    const float cy = c2 * ydot;
-    T* row = (T*)a.dh + ((int64_t)bh * a.Tq_pad + i) * DP;
-    T* col = (T*)a.dhT + (int64_t)bh * DP * a.Tq_pad + i;
-#pragma unroll
-    for (int d = 0; d < DP; ++d) x[d] = c1 * x[d] + cy * yv[d];
-#pragma unroll
-    for (int d = 0; d < DP; d += 4) store4(row + d, x[d], x[d + 1], x[d + 2], x[d + 3]);
-#pragma unroll
-    for (int d = 0; d < DP; ++d) col[(int64_t)d * a.Tq_pad] = from_f<T>(x[d]);
+// dh = F dy + G (h.dy) h with h = y/F  ->  dh = c1 dy + c2 (y.dy) y
+__device__ inline void tanhnorm_coefs(float n, float eps, float& c1, float& c2) {
+  if (n > eps) {
+    const float t = tanhf(n);
+    c1 = t / n;
+    c2 = tanhnorm_g(n, t) / (c1 * c1);
+  } else {
+    c1 = tanhf(eps) / eps;
+    c2 = 0.0f;
   }
 }
 
@@ -108,15 +57,72 @@ struct BwdKArgs {
   const void* q; Strides3 qs;
   const void* k; Strides3 ks;
   const void* v; Strides3 vs;
+  const uint8_t* kpm;
+  const void* y; const void* dy; const float* hnorm;
   const float* r; const float* w;
   const uint32_t* bits;
-  const void* khat; const void* khatT; const void* vhat;
-  const void* qhat; const void* qhatT; const void* dh; const void* dhT;
   void* dq; void* dk; void* dv; float* part;
   int B, H, Tq, Tk, D, nqt, nkt, nkt_words, causal;
-  int64_t Tq_pad, Tk_pad;
   float eps;
 };
+
+// Query-side rows for row i of head (b,h): raw q with 1/|q|, and dh.
+template <typename T, int DP>
+__device__ inline void query_rows(const BwdKArgs& a, int b, int h, int bh, int i, int half, Row<T, DP>& qr,
+                                  float& iq, Row<T, DP>& dh) {
+  const bool ok = i < a.Tq;
+  const int ii = ok ? i : 0;
+  qr.load((const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, ok, a.D, half);
+  iq = qr.inv_norm(a.eps);
+  const int64_t yoff = (((int64_t)b * a.Tq + ii) * a.H + h) * a.D;
+  Row<T, DP> yr;
+  yr.load((const T*)a.y + yoff, ok, a.D, half);
+  dh.load((const T*)a.dy + yoff, ok, a.D, half);
+  const float ydot = yr.dot(dh);
+  float c1, c2;
+  tanhnorm_coefs(ok ? a.hnorm[(int64_t)bh * a.Tq + ii] : 0.0f, a.eps, c1, c2);
+  const float cy = c2 * ydot;
+#pragma unroll
+  for (int n = 0; n < Row<T, DP>::N; ++n) dh.x[n] = c1 * dh.x[n] + cy * yr.x[n];
+}
+
+// Key-side rows for key j of head (b,h): raw k with 1/|k| (0 for padded or
+// masked keys) and raw v with 1/|v|.
+template <typename T, int DP>
+__device__ inline void key_rows(const BwdKArgs& a, int b, int h, int j, int half, Row<T, DP>& kr, float& ik,
+                                Row<T, DP>& vr, float& iv) {
+  const bool ok = j < a.Tk;
+  const int jj = ok ? j : 0;
+  kr.load((const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, ok, a.D, half);
+  vr.load((const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, ok, a.D, half);
+  ik = kr.inv_norm(a.eps);
+  iv = vr.inv_norm(a.eps);
+  if (!ok || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + jj])) ik = 0.0f;
+}
+
+// Writes the lane's slots of operand row `m` (rounded to T) into a transposed
+// LDS tile t[d][m] of pitch ld.
+template <typename T, int DP>
+__device__ inline void stash_transposed(T* t, int ld, int m, const Row<T, DP>& row, int half) {
+  constexpr int KS = Mma<T>::KS, PER = Mma<T>::PER, NKS = DP / KS;
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+    for (int e = 0; e < PER; ++e) t[(KS * ks + PER * half + e) * ld + m] = from_f<T>(row.x[ks * PER + e]);
+}
+
+// Scale factors of the 16 rows a lane's C-block registers cover:
+// register r -> row 16*(r/8) + 8*half + r%8 of a 32-row half tile.
+__device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]) {
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(sc + 16 * g + 8 * half + 4 * u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[8 * g + 4 * u + e] = v[e];
+    }
+}
 
 // Writes dx = normalise-backward(dx^, x) for one row held in C-layout
 // registers acc[dh] (rows d = 32*dh + 8*(r/4) + 4*half + r%4) of a lane.
@@ -161,37 +167,43 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[NDH], const T* xrow, b
     }
 }
 
-// Wave per 64-key tile kt of head (b,h); lane -> key j = k0 + 32*kh + l32.
+template <typename T>
+struct LdsT {
+  static constexpr int LD = 32 + 16 / (int)sizeof(T);  // padded pitch of a transposed half tile
+};
+
+// One wave (64-thread block) per 64-key tile of head (b,h); lane -> key
+// j = k0 + 32*kh + l32.
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void dkdv_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(64) void dkdv_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int half = lane >> 5, l32 = lane & 31;
-  const int kt = blockIdx.x * 4 + wave;
-  if (kt >= a.nkt) return;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  constexpr int LD = LdsT<T>::LD;
+  __shared__ __attribute__((aligned(16))) T tq[DP * LD];   // raw q^T [d][i]
+  __shared__ __attribute__((aligned(16))) T th[DP * LD];   // dh^T    [d][i]
+  __shared__ __attribute__((aligned(16))) float sq[32];    // 1/|q_i|
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  int kt, bh;
+  xcd_order(kt, bh);
+  const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
   const int k0 = kt * kTile;
 
-  const T* khat = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
-  const T* vhat = (const T*)a.vhat + (int64_t)bh * a.Tk_pad * DP;
-  const T* qhat = (const T*)a.qhat + (int64_t)bh * a.Tq_pad * DP;
-  const T* dh = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
-  const T* qhatT = (const T*)a.qhatT + (int64_t)bh * DP * a.Tq_pad;
-  const T* dhT = (const T*)a.dhT + (int64_t)bh * DP * a.Tq_pad;
-
+  // own keys as raw B operands, with their 1/|k| and 1/|v|
   frag kf[2][NKS], vf[2][NKS];
+  float ikl[2], ivl[2];
 #pragma unroll
-  for (int kh = 0; kh < 2; ++kh)
+  for (int kh = 0; kh < 2; ++kh) {
+    Row<T, DP> kr, vr;
+    key_rows<T, DP>(a, b, h, k0 + 32 * kh + l32, half, kr, ikl[kh], vr, ivl[kh]);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      const int64_t off = (int64_t)(k0 + 32 * kh + l32) * DP + KS * ks + PER * half;
-      kf[kh][ks] = M::load(khat + off);
-      vf[kh][ks] = M::load(vhat + off);
+      kf[kh][ks] = kr.frag(ks, 1.0f);
+      vf[kh][ks] = vr.frag(ks, 1.0f);
     }
+  }
 
   f32x16 adv[NDH][2], adk[NDH][2];
 #pragma unroll
@@ -209,82 +221,100 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdKArgs a) {
   if (ihi > a.Tq - 1) ihi = a.Tq - 1;
   const int qt_lo = (int)(ilo / kTile), qt_hi = ihi >= ilo ? (int)(ihi / kTile) : qt_lo - 1;
 
-  for (int qt = qt_lo; qt <= qt_hi; ++qt) {
-    const uint32_t word = a.bits[((int64_t)bh * a.nqt + qt) * a.nkt_words + (kt >> 5)];
-    if (((word >> (kt & 31)) & 1u) == 0u) continue;
-    const int q0 = qt * kTile;
-    f32x16 s[2][2], dp[2][2];
-#pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { s[qh][kh][r] = 0.0f; dp[qh][kh][r] = 0.0f; }
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
+  for (int base = qt_lo; base <= qt_hi; base += kWave) {
+    const int ql = base + lane;
+    bool bit = false;
+    if (ql <= qt_hi) bit = (a.bits[((int64_t)bh * a.nqt + ql) * a.nkt_words + (kt >> 5)] >> (kt & 31)) & 1u;
+    unsigned long long mask = __ballot(bit);
+    while (mask != 0ull) {
+      const int qt = base + __builtin_ctzll(mask);
+      mask &= mask - 1ull;
+      const int q0 = qt * kTile;
+
+      // one 32-row half of the query tile at a time
       for (int qh = 0; qh < 2; ++qh) {
-        const int64_t off = (int64_t)(q0 + 32 * qh + perm_row(l32)) * DP + KS * ks + PER * half;
-        const frag qa = M::load(qhat + off);
-        const frag ha = M::load(dh + off);
+        // rows i = q0 + 32*qh + perm_row(l32) as A operands; transposes and
+        // 1/|q| into LDS
+        frag qa[NKS], ha[NKS];
+        wave_lds_sync();
+        {
+          const int m = perm_row(l32);
+          Row<T, DP> qr, dr;
+          float iq;
+          query_rows<T, DP>(a, b, h, bh, q0 + 32 * qh + m, half, qr, iq, dr);
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          s[qh][kh] = M::mma(qa, kf[kh][ks], s[qh][kh]);
-          dp[qh][kh] = M::mma(ha, vf[kh][ks], dp[qh][kh]);
-        }
-      }
-    // pair weights P (into s) and ds (into dp)
-#pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const int j = k0 + 32 * kh + l32;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = q0 + 32 * qh + rowof(r, half);
-          const int64_t dd = (int64_t)i - j;
-          const float sv = s[qh][kh][r];
-          const float av = trim(sv, hp.r);
-          float p = 0.0f, ds = 0.0f;
-          if (av > 0.0f && in_window(dd, hp.wc, causal)) {
-            const float m = softmask(dd, hp.iw);
-            const float g = dp[qh][kh][r];
-            p = av * av * m;
-            ds = 2.0f * av * hp.r * m * g;
-            dr_acc -= 2.0f * av * (1.0f - sv) * m * g;
-            dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+          for (int ks = 0; ks < NKS; ++ks) {
+            qa[ks] = qr.frag(ks, 1.0f);
+            ha[ks] = dr.frag(ks, 1.0f);
           }
-          s[qh][kh][r] = p;
-          dp[qh][kh][r] = ds;
+          stash_transposed<T, DP>(tq, LD, m, qr, half);
+          stash_transposed<T, DP>(th, LD, m, dr, half);
+          if (half == 0) sq[m] = iq;
         }
-      }
-    // dv^T[d][j] += sum_i dh^T[d][i] P[i][j];  dk^T[d][j] += sum_i q^T[d][i] ds[i][j]
+        wave_lds_sync();
+        float isq[16];
+        read_row_scales(sq, half, isq);
+
+        f32x16 s[2], dp[2];
 #pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
+        for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int r0 = c * PER;
-        const int ioff = q0 + 32 * qh + rowof(r0, half);
-        frag ht[NDH], qT[NDH];
+          for (int r = 0; r < 16; ++r) { s[kh][r] = 0.0f; dp[kh][r] = 0.0f; }
 #pragma unroll
-        for (int dh_ = 0; dh_ < NDH; ++dh_) {
-          ht[dh_] = M::load(dhT + (int64_t)(32 * dh_ + l32) * a.Tq_pad + ioff);
-          qT[dh_] = M::load(qhatT + (int64_t)(32 * dh_ + l32) * a.Tq_pad + ioff);
-        }
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            s[kh] = M::mma(qa[ks], kf[kh][ks], s[kh]);
+            dp[kh] = M::mma(ha[ks], vf[kh][ks], dp[kh]);
+          }
+        // P (into s) and ds/|q| (into dp); register r -> query
+        // q0 + 32qh + 16(r/8) + 8half + r%8, lane -> key k0 + 32kh + l32
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          const frag pb = M::pack(s[qh][kh], r0);
-          const frag sb = M::pack(dp[qh][kh], r0);
+          const int rel0 = (q0 + 32 * qh + 8 * half) - (k0 + 32 * kh + l32);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dd = rel0 + 16 * (r >> 3) + (r & 7);
+            const float sv = s[kh][r] * isq[r] * ikl[kh];
+            const float av = trim(sv, hp.r);
+            const bool lv = av > 0.0f && in_window(dd, hp.wc, causal);
+            float p = 0.0f, ds = 0.0f;
+            if (__ballot(lv) != 0) {
+              if (lv) {
+                const float m = softmask(dd, hp.iw);
+                const float g = dp[kh][r] * ivl[kh];
+                p = av * av * m;
+                ds = 2.0f * av * hp.r * m * g;
+                dr_acc -= 2.0f * av * (1.0f - sv) * m * g;
+                dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+              }
+            }
+            s[kh][r] = p;
+            dp[kh][r] = ds * isq[r];
+          }
+        }
+        // dv^T[d][j] += sum_i dh^T[d][i] P[i][j];  dk^T[d][j] += sum_i q^T[d][i] (ds/|q|)[i][j]
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int r0 = c * PER;
+          const int ioff = rowof(r0, half);
 #pragma unroll
           for (int dh_ = 0; dh_ < NDH; ++dh_) {
-            adv[dh_][kh] = M::mma(ht[dh_], pb, adv[dh_][kh]);
-            adk[dh_][kh] = M::mma(qT[dh_], sb, adk[dh_][kh]);
+            const frag ht = M::load(&th[(32 * dh_ + l32) * LD + ioff]);
+            const frag qT = M::load(&tq[(32 * dh_ + l32) * LD + ioff]);
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+              adv[dh_][kh] = M::mma(ht, M::pack(s[kh], r0), adv[dh_][kh]);
+              adk[dh_][kh] = M::mma(qT, M::pack(dp[kh], r0), adk[dh_][kh]);
+            }
           }
         }
       }
+    }
   }
 
-  // Epilogue: normalisation backward for k and v, written to (B,Tk,H,D).
+  // Epilogue: dk^ = 1/|k| sum_i (ds/|q|) q and dv^ = 1/|v| ... -> fold the key's
+  // own scale, then the normalisation backward; written to (B,Tk,H,D).
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
     const int j = k0 + 32 * kh + l32;
@@ -310,36 +340,37 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdKArgs a) {
   }
 }
 
-// Wave per 64-query tile qt of head (b,h); lane -> query i = q0 + 32*qh + l32.
+// One wave (64-thread block) per 64-query tile of head (b,h); lane -> query
+// i = q0 + 32*qh + l32.
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void dq_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(64) void dq_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int half = lane >> 5, l32 = lane & 31;
-  const int qt = blockIdx.x * 4 + wave;
-  if (qt >= a.nqt) return;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  constexpr int LD = LdsT<T>::LD;
+  __shared__ __attribute__((aligned(16))) T tk[DP * LD];   // raw k^T [d][j]
+  __shared__ __attribute__((aligned(16))) float sk[32];    // 1/|k_j| (0 if masked)
+  __shared__ __attribute__((aligned(16))) float sv[32];    // 1/|v_j|
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  int qt, bh;
+  xcd_order(qt, bh);
+  const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
   const int q0 = qt * kTile;
 
-  const T* khat = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
-  const T* vhat = (const T*)a.vhat + (int64_t)bh * a.Tk_pad * DP;
-  const T* khatT = (const T*)a.khatT + (int64_t)bh * DP * a.Tk_pad;
-  const T* qhat = (const T*)a.qhat + (int64_t)bh * a.Tq_pad * DP;
-  const T* dh = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
-
   frag qb[2][NKS], hb[2][NKS];
+  float iql[2];
 #pragma unroll
-  for (int qh = 0; qh < 2; ++qh)
+  for (int qh = 0; qh < 2; ++qh) {
+    Row<T, DP> qr, dr;
+    query_rows<T, DP>(a, b, h, bh, q0 + 32 * qh + l32, half, qr, iql[qh], dr);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      const int64_t off = (int64_t)(q0 + 32 * qh + l32) * DP + KS * ks + PER * half;
-      qb[qh][ks] = M::load(qhat + off);
-      hb[qh][ks] = M::load(dh + off);
+      qb[qh][ks] = qr.frag(ks, 1.0f);
+      hb[qh][ks] = dr.frag(ks, 1.0f);
     }
+  }
   f32x16 adq[NDH][2];
 #pragma unroll
   for (int dh_ = 0; dh_ < NDH; ++dh_)
@@ -356,62 +387,81 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdKArgs a) {
   const int kt_lo = (int)(jlo / kTile), kt_hi = jhi >= jlo ? (int)(jhi / kTile) : kt_lo - 1;
   const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
 
-  for (int kt = kt_lo; kt <= kt_hi; ++kt) {
-    if (((brow[kt >> 5] >> (kt & 31)) & 1u) == 0u) continue;
-    const int k0 = kt * kTile;
-    f32x16 s[2][2], dp[2][2];
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { s[kh][qh][r] = 0.0f; dp[kh][qh][r] = 0.0f; }
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
+  for (int base = kt_lo; base <= kt_hi; base += kWave) {
+    const int kl = base + lane;
+    const bool bit = kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u);
+    unsigned long long mask = __ballot(bit);
+    while (mask != 0ull) {
+      const int kt = base + __builtin_ctzll(mask);
+      mask &= mask - 1ull;
+      const int k0 = kt * kTile;
+
+      // one 32-key half of the key tile at a time
       for (int kh = 0; kh < 2; ++kh) {
-        const int64_t off = (int64_t)(k0 + 32 * kh + perm_row(l32)) * DP + KS * ks + PER * half;
-        const frag ka = M::load(khat + off);
-        const frag va = M::load(vhat + off);
+        // key rows j = k0 + 32*kh + perm_row(l32) as A operands; k^T and the
+        // key scales into LDS
+        frag ka[NKS], va[NKS];
+        wave_lds_sync();
+        {
+          const int m = perm_row(l32);
+          Row<T, DP> kr, vr;
+          float ik, iv;
+          key_rows<T, DP>(a, b, h, k0 + 32 * kh + m, half, kr, ik, vr, iv);
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            ka[ks] = kr.frag(ks, 1.0f);
+            va[ks] = vr.frag(ks, 1.0f);
+          }
+          stash_transposed<T, DP>(tk, LD, m, kr, half);
+          if (half == 0) { sk[m] = ik; sv[m] = iv; }
+        }
+        wave_lds_sync();
+        float isk[16], isv[16];
+        read_row_scales(sk, half, isk);
+        read_row_scales(sv, half, isv);
+
+        f32x16 s[2], dp[2];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) { s[qh][r] = 0.0f; dp[qh][r] = 0.0f; }
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+          for (int qh = 0; qh < 2; ++qh) {
+            s[qh] = M::mma(ka[ks], qb[qh][ks], s[qh]);
+            dp[qh] = M::mma(va[ks], hb[qh][ks], dp[qh]);
+          }
+        // (ds/|k|)^T; register r -> key k0 + 32kh + 16(r/8) + 8half + r%8, lane -> query
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
-          s[kh][qh] = M::mma(ka, qb[qh][ks], s[kh][qh]);
-          dp[kh][qh] = M::mma(va, hb[qh][ks], dp[kh][qh]);
+          const int rel0 = (q0 + 32 * qh + l32) - (k0 + 32 * kh + 8 * half);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+            const float av = trim(s[qh][r] * isk[r] * iql[qh], hp.r);
+            const bool lv = av > 0.0f && in_window(dd, hp.wc, causal);
+            float ds = 0.0f;
+            if (__ballot(lv) != 0) {
+              if (lv) ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[qh][r] * isv[r];
+            }
+            dp[qh][r] = ds * isk[r];
+          }
+        }
+        // dq^T[d][i] += sum_j k^T[d][j] (ds/|k|)^T[j][i]
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int r0 = c * PER;
+          const int koff = rowof(r0, half);
+#pragma unroll
+          for (int dh_ = 0; dh_ < NDH; ++dh_) {
+            const frag kT = M::load(&tk[(32 * dh_ + l32) * LD + koff]);
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) adq[dh_][qh] = M::mma(kT, M::pack(dp[qh], r0), adq[dh_][qh]);
+          }
         }
       }
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int qh = 0; qh < 2; ++qh) {
-        const int i = q0 + 32 * qh + l32;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = k0 + 32 * kh + rowof(r, half);
-          const int64_t dd = (int64_t)i - j;
-          const float av = trim(s[kh][qh][r], hp.r);
-          float ds = 0.0f;
-          if (av > 0.0f && in_window(dd, hp.wc, causal))
-            ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[kh][qh][r];
-          dp[kh][qh][r] = ds;
-        }
-      }
-    // dq^T[d][i] += sum_j k^T[d][j] ds^T[j][i]
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int r0 = c * PER;
-        const int koff = k0 + 32 * kh + rowof(r0, half);
-        frag kT[NDH];
-#pragma unroll
-        for (int dh_ = 0; dh_ < NDH; ++dh_) kT[dh_] = M::load(khatT + (int64_t)(32 * dh_ + l32) * a.Tk_pad + koff);
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {
-          const frag sb = M::pack(dp[kh][qh], r0);
-#pragma unroll
-          for (int dh_ = 0; dh_ < NDH; ++dh_) adq[dh_][qh] = M::mma(kT[dh_], sb, adq[dh_][qh]);
-        }
-      }
+    }
   }
 
 #pragma unroll
@@ -454,61 +504,33 @@ __global__ __launch_bounds__(256) void rw_reduce_kernel(const float* part, float
 }
 
 size_t bwd_ws_bytes(const Geometry& g) {
-  const size_t one = (size_t)g.B * g.H * g.Tq_pad * g.DP * g.esize;
-  const size_t part = (size_t)2 * g.B * g.H * g.nkt * sizeof(float);
-  return 4 * one + round_up((int64_t)part, 256);
-}
-
-BwdWs bwd_ws_carve(const Geometry& g, void* base) {
-  const size_t one = (size_t)g.B * g.H * g.Tq_pad * g.DP * g.esize;
-  char* p = (char*)base;
-  BwdWs ws;
-  ws.qhat = p;
-  ws.qhatT = p + one;
-  ws.dh = p + 2 * one;
-  ws.dhT = p + 3 * one;
-  ws.part = (float*)(p + 4 * one);
-  return ws;
+  return round_up((int64_t)2 * g.B * g.H * g.nkt * (int64_t)sizeof(float), 256);
 }
 
 template <typename T, int DP>
 static hipError_t launch_bwd_t(const BwdCall& c) {
   const Geometry& g = c.g;
-  BwdPrepArgs pa;
-  pa.q = c.q; pa.qs = c.qs; pa.y = c.y; pa.dy = c.dy; pa.hnorm = c.hnorm;
-  pa.qhat = c.bws.qhat; pa.qhatT = c.bws.qhatT; pa.dh = c.bws.dh; pa.dhT = c.bws.dhT;
-  pa.H = g.H; pa.Tq = g.Tq; pa.D = g.D; pa.Tq_pad = g.Tq_pad; pa.eps = c.eps;
-  timer_begin(3, c.stream);
-  hipLaunchKernelGGL((bwd_prep_kernel<T, DP>), dim3((unsigned)(g.Tq_pad / 64), (unsigned)(g.B * g.H)), dim3(64), 0,
-                     c.stream, pa);
-  timer_end(3, c.stream);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-
   BwdKArgs ka;
-  ka.q = c.q; ka.qs = c.qs; ka.k = c.k; ka.ks = c.ks; ka.v = c.v; ka.vs = c.vs;
+  ka.q = c.q; ka.qs = c.qs; ka.k = c.k; ka.ks = c.ks; ka.v = c.v; ka.vs = c.vs; ka.kpm = c.kpm;
+  ka.y = c.y; ka.dy = c.dy; ka.hnorm = c.hnorm;
   ka.r = c.r; ka.w = c.w; ka.bits = c.bits;
-  ka.khat = c.fws.khat; ka.khatT = c.fws.khatT; ka.vhat = c.fws.vhat;
-  ka.qhat = c.bws.qhat; ka.qhatT = c.bws.qhatT; ka.dh = c.bws.dh; ka.dhT = c.bws.dhT;
-  ka.dq = c.dq; ka.dk = c.dk; ka.dv = c.dv; ka.part = c.bws.part;
+  ka.dq = c.dq; ka.dk = c.dk; ka.dv = c.dv; ka.part = c.part;
   ka.B = g.B; ka.H = g.H; ka.Tq = g.Tq; ka.Tk = g.Tk; ka.D = g.D;
   ka.nqt = g.nqt; ka.nkt = g.nkt; ka.nkt_words = g.nkt_words; ka.causal = g.causal;
-  ka.Tq_pad = g.Tq_pad; ka.Tk_pad = g.Tk_pad; ka.eps = c.eps;
+  ka.eps = c.eps;
   timer_begin(4, c.stream);
-  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)((g.nkt + 3) / 4), (unsigned)(g.B * g.H)), dim3(256), 0,
-                     c.stream, ka);
+  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)g.nkt, (unsigned)(g.B * g.H)), dim3(64), 0, c.stream, ka);
   timer_end(4, c.stream);
-  e = hipGetLastError();
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(5, c.stream);
-  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)((g.nqt + 3) / 4), (unsigned)(g.B * g.H)), dim3(256), 0,
-                     c.stream, ka);
+  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(64), 0, c.stream, ka);
   timer_end(5, c.stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(6, c.stream);
-  hipLaunchKernelGGL(rw_reduce_kernel, dim3((unsigned)g.H), dim3(256), 0, c.stream, (const float*)c.bws.part, c.dr,
-                     c.dw, g.B, g.H, g.nkt);
+  hipLaunchKernelGGL(rw_reduce_kernel, dim3((unsigned)g.H), dim3(256), 0, c.stream, (const float*)c.part, c.dr, c.dw,
+                     g.B, g.H, g.nkt);
   timer_end(6, c.stream);
   return hipGetLastError();
 }

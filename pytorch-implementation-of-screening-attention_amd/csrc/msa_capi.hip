@@ -112,7 +112,7 @@ int msa_timer_arm(int kernel, int n) {
   t.kernel = 0;
   t.next = 0;
   if (kernel == 0 || n <= 0) return ok();
-  if (kernel < MSA_K_PREP_KV || kernel > MSA_K_DECODE) return fail(MSA_ERR_INVALID, "unknown kernel id %d", kernel);
+  if (kernel < MSA_K_PREP_K || kernel > MSA_K_DECODE) return fail(MSA_ERR_INVALID, "unknown kernel id %d", kernel);
   for (int i = 0; i < n; ++i) {
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
@@ -140,10 +140,10 @@ int msa_version(void) { return (0 << 16) | (1 << 8) | 0; }
 
 const char* msa_last_error(void) { return g_last_error.c_str(); }
 
-size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype, int need_bwd) {
+size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype) {
   msa::Geometry g;
   if (check_geometry(B, H, Tq, Tk, D, dtype, 1, &g) != MSA_OK) return 0;
-  return msa::fwd_ws_bytes(g, need_bwd);
+  return msa::fwd_ws_bytes(g);
 }
 
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk) {
@@ -162,7 +162,7 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
             int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int Tq, int Tk,
             int D, int dtype, const float* r, const float* w, const uint8_t* key_padding_mask, int causal, float eps,
             void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words, void* workspace,
-            size_t workspace_bytes, int need_bwd, void* stream) {
+            size_t workspace_bytes, void* stream) {
   msa::Geometry g;
   int rc = check_geometry(B, H, Tq, Tk, D, dtype, causal, &g);
   if (rc != MSA_OK) return rc;
@@ -180,7 +180,7 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
   if (tile_bits_words < msa_tile_bits_words(B, H, Tq, Tk))
     return fail(MSA_ERR_WORKSPACE, "tile_bits holds %zu words, %zu needed", tile_bits_words,
                 msa_tile_bits_words(B, H, Tq, Tk));
-  const size_t need = msa::fwd_ws_bytes(g, need_bwd);
+  const size_t need = msa::fwd_ws_bytes(g);
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(MSA_ERR_WORKSPACE, "forward workspace holds %zu bytes, %zu needed", workspace_bytes, need);
   if (need > 0 && !aligned16(workspace)) return fail(MSA_ERR_INVALID, "workspace is not 16-byte aligned");
@@ -192,18 +192,17 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
   c.v = v; c.vs = {v_sb, v_st, v_sh};
   c.r = r; c.w = w; c.kpm = key_padding_mask; c.eps = eps;
   c.y = y; c.hnorm = hnorm; c.bits = tile_bits;
-  c.ws = msa::fwd_ws_carve(g, workspace, need_bwd);
-  c.need_bwd = need_bwd;
+  c.khat = workspace;
   c.stream = (hipStream_t)stream;
   return hip_status(msa::launch_fwd(c), "msa_fwd launch");
 }
 
 int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_st,
             int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int Tq, int Tk,
-            int D, int dtype, const float* r, const float* w, int causal, float eps, const void* y,
-            const float* hnorm, const void* dy, const uint32_t* tile_bits, size_t tile_bits_words,
-            const void* fwd_workspace, size_t fwd_workspace_bytes, void* dq, void* dk, void* dv, float* dr,
-            float* dw, void* workspace, size_t workspace_bytes, void* stream) {
+            int D, int dtype, const float* r, const float* w, const uint8_t* key_padding_mask, int causal, float eps,
+            const void* y, const float* hnorm, const void* dy, const uint32_t* tile_bits, size_t tile_bits_words,
+            void* dq, void* dk, void* dv, float* dr, float* dw, void* workspace, size_t workspace_bytes,
+            void* stream) {
   msa::Geometry g;
   int rc = check_geometry(B, H, Tq, Tk, D, dtype, causal, &g);
   if (rc != MSA_OK) return rc;
@@ -224,25 +223,19 @@ int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
   if (tile_bits_words < msa_tile_bits_words(B, H, Tq, Tk))
     return fail(MSA_ERR_WORKSPACE, "tile_bits holds %zu words, %zu needed", tile_bits_words,
                 msa_tile_bits_words(B, H, Tq, Tk));
-  const size_t fneed = msa::fwd_ws_bytes(g, 1);
-  if (fwd_workspace == nullptr || fwd_workspace_bytes < fneed)
-    return fail(MSA_ERR_WORKSPACE, "forward workspace holds %zu bytes, %zu needed (msa_fwd with need_bwd=1)",
-                fwd_workspace_bytes, fneed);
   const size_t need = msa::bwd_ws_bytes(g);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(MSA_ERR_WORKSPACE, "backward workspace holds %zu bytes, %zu needed", workspace_bytes, need);
-  if (!aligned16(workspace) || !aligned16(fwd_workspace))
-    return fail(MSA_ERR_INVALID, "workspaces must be 16-byte aligned");
+  if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "workspace is not 16-byte aligned");
 
   msa::BwdCall c;
   c.g = g;
   c.q = q; c.qs = {q_sb, q_st, q_sh};
   c.k = k; c.ks = {k_sb, k_st, k_sh};
   c.v = v; c.vs = {v_sb, v_st, v_sh};
-  c.r = r; c.w = w; c.eps = eps;
+  c.r = r; c.w = w; c.kpm = key_padding_mask; c.eps = eps;
   c.y = y; c.hnorm = hnorm; c.dy = dy; c.bits = tile_bits;
-  c.fws = msa::fwd_ws_carve(g, const_cast<void*>(fwd_workspace), 1);
-  c.bws = msa::bwd_ws_carve(g, workspace);
+  c.part = (float*)workspace;
   c.dq = dq; c.dk = dk; c.dv = dv; c.dr = dr; c.dw = dw;
   c.stream = (hipStream_t)stream;
   return hip_status(msa::launch_bwd(c), "msa_bwd launch");

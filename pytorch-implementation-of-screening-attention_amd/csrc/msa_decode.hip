@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
         const float av = trim(s, hp.r);
         const int64_t j = base + u * KPW + kl;
         if (ok[u] && av > 0.0f) {
-          const float m = softmask(pos - j, hp.iw);
+          const float m = softmask((int)(pos - j), hp.iw);
           const T* vp = vb + j * a.vs.st;
           float vv[VEC], vs2 = 0.0f;
 #pragma unroll

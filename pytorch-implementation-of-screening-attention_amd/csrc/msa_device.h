@@ -25,15 +25,32 @@ constexpr int kTile = 64;  // rows of a query tile and of a key tile
 // contraction whose A and B slots are filled for the same logical k is exact
 // whatever that mapping is.
 //   C/D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+//
+// Source-operand guard.  With this toolchain (ROCm 7.2 clang, gfx950) a VALU
+// instruction may be scheduled to overwrite the A/B source VGPRs of a
+// v_mfma_f32_32x32x16_bf16 within a few cycles of its issue, with no wait
+// states in between, and the MFMA then reads the new values: measured on an
+// MI355X, 2 and 4 wait states still corrupted the product, 8 did not.  After
+// every MFMA an s_nop block that takes A and B as read-write operands keeps
+// those registers from being reused until 16 wait states have passed.  The
+// MFMA pipe is busy far longer than that per instruction, so back-to-back
+// MFMA throughput is unchanged.
 // ---------------------------------------------------------------------------
 template <typename T> struct Mma;
+
+template <typename F>
+__device__ inline void guard_mfma_sources(F& a, F& b) {
+  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
+}
 
 template <> struct Mma<bf16> {
   static constexpr int KS = 16;
   static constexpr int PER = 8;
   typedef bf16x8 frag;
   __device__ static inline f32x16 mma(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    guard_mfma_sources(a, b);
+    return d;
   }
   __device__ static inline frag load(const bf16* p) { return *reinterpret_cast<const frag*>(p); }
   __device__ static inline frag zero() { frag z; for (int e = 0; e < 8; ++e) z[e] = (bf16)0.0f; return z; }
@@ -52,7 +69,9 @@ template <> struct Mma<float> {
   static constexpr int PER = 1;
   typedef float frag;
   __device__ static inline f32x16 mma(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    guard_mfma_sources(a, b);
+    return d;
   }
   __device__ static inline frag load(const float* p) { return *p; }
   __device__ static inline frag zero() { return 0.0f; }
@@ -79,7 +98,7 @@ struct HeadParams {
   float r;     // acceptance sharpness r_h > 1 (may round to 1.0f)
   float w;     // window w_h > 1
   float iw;    // 1/w
-  int64_t wc;  // ceil(w): for integer distance d, d < w  <=>  d < wc
+  int wc;      // ceil(w) (capped at 2^30): for integer distance d, d < w  <=>  d < wc
 };
 
 __device__ inline HeadParams head_params(const float* r, const float* w, int h) {
@@ -88,13 +107,13 @@ __device__ inline HeadParams head_params(const float* r, const float* w, int h) 
   p.w = w[h];
   p.iw = 1.0f / p.w;
   float c = ceilf(p.w);
-  p.wc = c > 1.0e9f ? (int64_t)1000000000 : (int64_t)c;
+  p.wc = c > 1073741824.0f ? 1073741824 : (int)c;
   return p;
 }
 
 // In-window test on the integer distance dd = i - j (attention.py:111-118 causal,
-// :176-181 non-causal).
-__device__ inline bool in_window(int64_t dd, int64_t wc, bool causal) {
+// :176-181 non-causal).  Positions stay below 2^22, so int arithmetic is exact.
+__device__ inline bool in_window(int dd, int wc, bool causal) {
   return causal ? (dd >= 0 && dd < wc) : (dd < wc && -dd < wc);
 }
 
@@ -103,11 +122,11 @@ __device__ inline float trim(float s, float r) { return 1.0f - r * (1.0f - s); }
 
 // Cosine soft mask m = (cos(pi (j-i)/w) + 1)/2 (attention.py:114) and its
 // derivative with respect to w, for an in-window distance dd = i - j.
-__device__ inline float softmask(int64_t dd, float iw) {
+__device__ inline float softmask(int dd, float iw) {
   const float x = (float)(-dd) * iw;
   return 0.5f * (cospif(x) + 1.0f);
 }
-__device__ inline float softmask_dw(int64_t dd, float iw) {
+__device__ inline float softmask_dw(int dd, float iw) {
   // d/dw [ (cos(pi rel/w)+1)/2 ] = sin(pi rel/w) * pi * rel / (2 w^2),  rel = j - i
   const float rel = (float)(-dd);
   const float x = rel * iw;
@@ -148,6 +167,64 @@ __device__ inline f32x4 load4(const bf16* p) {
 
 __device__ inline int64_t floordiv(int64_t a, int64_t b) {  // b > 0
   return a >= 0 ? a / b : -((-a + b - 1) / b);
+}
+
+// ---------------------------------------------------------------------------
+// Operand rows.  A lane that supplies row m of an operand holds its NKS slot
+// groups: d = KS*ks + PER*half + e.  Its partner lane (lane ^ 32) holds the
+// other half of the row, so row reductions take one cross-half shuffle.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+struct Row {
+  static constexpr int KS = Mma<T>::KS, PER = Mma<T>::PER, NKS = DP / KS, N = NKS * PER;
+  float x[N];
+
+  // Loads the lane's slots of row `p` (D valid columns); zeros when !ok.
+  __device__ inline void load(const T* p, bool ok, int D, int half) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = KS * ks + PER * half;
+      const bool in = ok && d0 < D;
+      const typename Mma<T>::frag f = in ? Mma<T>::load(p + d0) : Mma<T>::zero();
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[ks * PER + e] = Mma<T>::get(f, e);
+    }
+  }
+  // Full-row dot product with another row held by the same lanes.
+  __device__ inline float dot(const Row& o) const {
+    float s = 0.0f;
+#pragma unroll
+    for (int n = 0; n < N; ++n) s += x[n] * o.x[n];
+    return s + __shfl_xor(s, 32);
+  }
+  __device__ inline float inv_norm(float eps) const { return 1.0f / fmaxf(sqrtf(dot(*this)), eps); }
+  // Operand fragment of slot group ks scaled by c.
+  __device__ inline typename Mma<T>::frag frag(int ks, float c) const {
+    f32x16 t;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) t[e] = x[ks * PER + e] * c;
+    return Mma<T>::pack(t, 0);
+  }
+};
+
+// Waits for this wave's LDS traffic and keeps the compiler from moving
+// memory operations across the point (LDS ops of one wave run in order).
+__device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs
+// in linear order (x fastest); when the grid divides evenly, remap so each
+// XCD receives a contiguous run of logical blocks (the query tiles of the same
+// heads share that XCD's L2).  Logical x is reversed so the longest causal
+// rows start first.
+__device__ inline void xcd_order(int& bx, int& by) {
+  const int nx = gridDim.x, N = gridDim.x * gridDim.y;
+  int p = blockIdx.x + nx * blockIdx.y;
+  if ((N & 7) == 0) {
+    const int per = N >> 3;
+    p = (p & 7) * per + (p >> 3);
+  }
+  by = p / nx;
+  bx = nx - 1 - (p - by * nx);
 }
 
 }  // namespace msa

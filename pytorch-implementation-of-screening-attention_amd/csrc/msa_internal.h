@@ -22,26 +22,12 @@ struct Geometry {
 
 struct Strides3 { int64_t sb, st, sh; };
 
-// Forward workspace (normalised key/value copies), each (B*H) x ... :
-//   khat  [bh][Tk_pad][DP]   row layout           (always)
-//   vhatT [bh][DP][Tk_pad]   transposed           (always)
-//   khatT [bh][DP][Tk_pad]   transposed           (need_bwd)
-//   vhat  [bh][Tk_pad][DP]   row layout           (need_bwd)
-struct FwdWs {
-  void* khat; void* vhatT; void* khatT; void* vhat;
-};
-size_t fwd_ws_bytes(const Geometry& g, int need_bwd);
-FwdWs fwd_ws_carve(const Geometry& g, void* base, int need_bwd);
+// Forward workspace: khat [b*h][Tk_pad][DP], unit-normalised K rows (zero for
+// padded and masked keys) that the forward stages through LDS.
+size_t fwd_ws_bytes(const Geometry& g);
 
-// Backward workspace:
-//   qhat  [bh][Tq_pad][DP], qhatT [bh][DP][Tq_pad]
-//   dh    [bh][Tq_pad][DP], dhT   [bh][DP][Tq_pad]
-//   part  [2][bh][nkt] fp32 per-wave partial sums of dr and dw
-struct BwdWs {
-  void* qhat; void* qhatT; void* dh; void* dhT; float* part;
-};
+// Backward workspace: part [2][b*h][nkt] fp32 per-wave partial sums of dr, dw.
 size_t bwd_ws_bytes(const Geometry& g);
-BwdWs bwd_ws_carve(const Geometry& g, void* base);
 
 struct FwdCall {
   Geometry g;
@@ -51,7 +37,7 @@ struct FwdCall {
   const float* r; const float* w; const uint8_t* kpm;
   float eps;
   void* y; float* hnorm; uint32_t* bits;
-  FwdWs ws; int need_bwd;
+  void* khat;
   hipStream_t stream;
 };
 hipError_t launch_fwd(const FwdCall& c);
@@ -61,11 +47,11 @@ struct BwdCall {
   const void* q; Strides3 qs;
   const void* k; Strides3 ks;
   const void* v; Strides3 vs;
-  const float* r; const float* w;
+  const float* r; const float* w; const uint8_t* kpm;
   float eps;
   const void* y; const float* hnorm; const void* dy;
   const uint32_t* bits;
-  FwdWs fws; BwdWs bws;
+  float* part;
   void* dq; void* dk; void* dv; float* dr; float* dw;
   hipStream_t stream;
 };

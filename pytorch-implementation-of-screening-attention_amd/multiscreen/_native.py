@@ -14,7 +14,7 @@ MSA_F32 = 0
 MSA_BF16 = 1
 
 # kernel ids for msa_timer_arm (include/msa.h)
-K_PREP_KV, K_FWD, K_BWD_PREP, K_DKDV, K_DQ, K_RW_REDUCE, K_DECODE = 1, 2, 3, 4, 5, 6, 7
+K_PREP_K, K_FWD, K_DKDV, K_DQ, K_RW_REDUCE, K_DECODE = 1, 2, 4, 5, 6, 7
 
 _lock = threading.Lock()
 _lib = None
@@ -28,15 +28,15 @@ _sz = ctypes.c_size_t
 _SIGS = {
     "msa_version": (_i, []),
     "msa_last_error": (ctypes.c_char_p, []),
-    "msa_fwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
+    "msa_fwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "msa_tile_bits_words": (_sz, [_i, _i, _i, _i]),
     "msa_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "msa_fwd": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                      _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _f,
-                     _p, _p, _p, _sz, _p, _sz, _i, _p]),
+                     _p, _p, _p, _sz, _p, _sz, _p]),
     "msa_bwd": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
-                     _i, _i, _i, _i, _i, _i, _p, _p, _i, _f,
-                     _p, _p, _p, _p, _sz, _p, _sz,
+                     _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _f,
+                     _p, _p, _p, _p, _sz,
                      _p, _p, _p, _p, _p, _p, _sz, _p]),
     "msa_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "msa_decode": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,

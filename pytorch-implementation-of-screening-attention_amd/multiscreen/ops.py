@@ -47,8 +47,16 @@ def tile_bits_words(B, H, Tq, Tk):
     return int(_native.lib().msa_tile_bits_words(B, H, Tq, Tk))
 
 
-def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, need_bwd=True):
-    """One msa_fwd call.  Returns (y, hnorm, tile_bits, workspace).
+def _kpm_u8(key_padding_mask, B, Tk, dev):
+    if key_padding_mask is None:
+        return None
+    if key_padding_mask.shape != (B, Tk):
+        raise ValueError(f"key_padding_mask must have shape ({B}, {Tk})")
+    return key_padding_mask.to(device=dev, dtype=torch.uint8).contiguous()
+
+
+def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None):
+    """One msa_fwd call.  Returns (y, hnorm, tile_bits).
 
     q (B,Tq,H,D), k/v (B,Tk,H,D) in float32 or bfloat16 on one GPU; r, w (H,).
     """
@@ -69,27 +77,23 @@ def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, need_bw
     dev = q.device
     r32 = r.detach().to(device=dev, dtype=torch.float32).contiguous()
     w32 = w.detach().to(device=dev, dtype=torch.float32).contiguous()
-    kpm = None
-    if key_padding_mask is not None:
-        if key_padding_mask.shape != (B, Tk):
-            raise ValueError(f"key_padding_mask must have shape ({B}, {Tk})")
-        kpm = key_padding_mask.to(device=dev, dtype=torch.uint8).contiguous()
+    kpm = _kpm_u8(key_padding_mask, B, Tk, dev)
     y = torch.empty((B, Tq, H, D), dtype=q.dtype, device=dev)
     hnorm = torch.empty((B, H, Tq), dtype=torch.float32, device=dev)
     nwords = tile_bits_words(B, H, Tq, Tk)
     bits = torch.empty((max(nwords, 1),), dtype=torch.int32, device=dev)
-    wsb = int(L.msa_fwd_workspace_bytes(B, H, Tq, Tk, D, dt, int(need_bwd)))
+    wsb = int(L.msa_fwd_workspace_bytes(B, H, Tq, Tk, D, dt))
     ws = torch.empty((max(wsb, 16),), dtype=torch.uint8, device=dev)
     rc = L.msa_fwd(*_args_bthd(q), *_args_bthd(k), *_args_bthd(v),
                    B, H, Tq, Tk, D, dt, r32.data_ptr(), w32.data_ptr(),
                    kpm.data_ptr() if kpm is not None else None, int(bool(causal)), float(eps),
                    y.data_ptr(), hnorm.data_ptr(), bits.data_ptr(), nwords,
-                   ws.data_ptr(), wsb, int(need_bwd), _stream_ptr(dev))
+                   ws.data_ptr(), wsb, _stream_ptr(dev))
     _native.check(rc, "msa_fwd")
-    return y, hnorm, bits, ws
+    return y, hnorm, bits
 
 
-def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, fws, dy):
+def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, dy, key_padding_mask=None):
     """One msa_bwd call.  Returns (dq, dk, dv, dr, dw); dq/dk/dv in (B,T,H,D)."""
     L = _native.lib()
     dt = _DTYPES[q.dtype]
@@ -98,7 +102,7 @@ def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, fws, dy):
     B, Tq, H, D = q.shape
     Tk = k.shape[1]
     dev = q.device
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dq = torch.empty((B, Tq, H, D), dtype=q.dtype, device=dev)
     dk = torch.empty((B, Tk, H, D), dtype=q.dtype, device=dev)
     dv = torch.empty((B, Tk, H, D), dtype=q.dtype, device=dev)
     dr = torch.empty((H,), dtype=torch.float32, device=dev)
@@ -108,12 +112,14 @@ def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, fws, dy):
     dy = dy.to(q.dtype).contiguous()
     r32 = r.detach().to(device=dev, dtype=torch.float32).contiguous()
     w32 = w.detach().to(device=dev, dtype=torch.float32).contiguous()
+    kpm = _kpm_u8(key_padding_mask, B, Tk, dev)
     wsb = int(L.msa_bwd_workspace_bytes(B, H, Tq, Tk, D, dt))
     ws = torch.empty((max(wsb, 16),), dtype=torch.uint8, device=dev)
     rc = L.msa_bwd(*_args_bthd(q), *_args_bthd(k), *_args_bthd(v),
-                   B, H, Tq, Tk, D, dt, r32.data_ptr(), w32.data_ptr(), int(bool(causal)), float(eps),
+                   B, H, Tq, Tk, D, dt, r32.data_ptr(), w32.data_ptr(),
+                   kpm.data_ptr() if kpm is not None else None, int(bool(causal)), float(eps),
                    y.data_ptr(), hnorm.data_ptr(), dy.data_ptr(), bits.data_ptr(),
-                   tile_bits_words(B, H, Tq, Tk), fws.data_ptr(), fws.numel(),
+                   tile_bits_words(B, H, Tq, Tk),
                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dr.data_ptr(), dw.data_ptr(),
                    ws.data_ptr(), wsb, _stream_ptr(dev))
     _native.check(rc, "msa_bwd")
@@ -125,18 +131,17 @@ class ScreeningCoreFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, r, w, causal, eps, key_padding_mask):
-        need_bwd = any(ctx.needs_input_grad[:5])
-        y, hnorm, bits, ws = fwd_raw(q, k, v, r, w, causal, eps, key_padding_mask, need_bwd=need_bwd)
-        if need_bwd:
-            ctx.save_for_backward(q, k, v, r, w, y, hnorm, bits, ws)
+        y, hnorm, bits = fwd_raw(q, k, v, r, w, causal, eps, key_padding_mask)
+        if any(ctx.needs_input_grad[:5]):
+            ctx.save_for_backward(q, k, v, r, w, y, hnorm, bits, key_padding_mask)
         ctx.causal = causal
         ctx.eps = eps
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        q, k, v, r, w, y, hnorm, bits, ws = ctx.saved_tensors
-        dq, dk, dv, dr, dw = bwd_raw(q, k, v, r, w, ctx.causal, ctx.eps, y, hnorm, bits, ws, dy)
+        q, k, v, r, w, y, hnorm, bits, kpm = ctx.saved_tensors
+        dq, dk, dv, dr, dw = bwd_raw(q, k, v, r, w, ctx.causal, ctx.eps, y, hnorm, bits, dy, kpm)
         return dq, dk, dv, dr.to(r.dtype), dw.to(w.dtype), None, None, None
 
 

@@ -33,28 +33,28 @@ def test_library_loads_and_exports_header():
 def test_version_and_sizes():
     L = _native.lib()
     assert L.msa_version() == (0 << 16) | (1 << 8)
-    # B=4, T=8192, H=8, D=64 bf16: K^, V^T (+ K^T, V^ for backward)
+    # B=4, T=8192, H=8, D=64 bf16: one normalised K^ copy, kept for the backward
     one = 4 * 8 * 8192 * 64 * 2
-    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1, 0) == 2 * one
-    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1, 1) == 4 * one
+    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == one
     assert L.msa_tile_bits_words(4, 8, 8192, 8192) == 4 * 8 * 128 * 4
     assert L.msa_tile_bits_words(1, 1, 65, 65) == 2
     # D=16 is padded to 32 in the workspace
-    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0, 0) == 2 * 64 * 32 * 4
-    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 48, 0, 0) == 0       # invalid D
+    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4
+    # backward workspace: (dr, dw) partial per (b, h, key tile)
+    assert L.msa_bwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == 2 * 4 * 8 * 128 * 4
+    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 48, 0) == 0       # invalid D
     assert L.msa_decode_workspace_bytes(16, 8, 64, 100000) == 16 * 8 * 49 * 64 * 4
 
 
 def _fwd(L, **kw):
     a = dict(q=16, qs=(1024, 64, 8), k=16, ks=(1024, 64, 8), v=16, vs=(1024, 64, 8),
              B=1, H=8, Tq=16, Tk=16, D=8 * 8, dtype=1, r=16, w=16, kpm=None, causal=1, eps=1e-8,
-             y=16, hnorm=16, bits=16, nbits=8, ws=16, wsb=1 << 30, need_bwd=1, stream=None)
+             y=16, hnorm=16, bits=16, nbits=8, ws=16, wsb=1 << 30, stream=None)
     a["D"] = 64
     a.update(kw)
     return L.msa_fwd(a["q"], *a["qs"], a["k"], *a["ks"], a["v"], *a["vs"], a["B"], a["H"], a["Tq"],
                      a["Tk"], a["D"], a["dtype"], a["r"], a["w"], a["kpm"], a["causal"], a["eps"],
-                     a["y"], a["hnorm"], a["bits"], a["nbits"], a["ws"], a["wsb"], a["need_bwd"],
-                     a["stream"])
+                     a["y"], a["hnorm"], a["bits"], a["nbits"], a["ws"], a["wsb"], a["stream"])
 
 
 @pytest.mark.parametrize("kw,code,msg", [
@@ -86,9 +86,12 @@ def test_fwd_empty_batch_is_a_no_op():
 
 def test_bwd_and_decode_reject_bad_arguments():
     L = _native.lib()
-    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, 1, 1e-8,
-                   16, 16, 16, 16, 1, 16, 10, 16, 16, 16, 16, 16, 16, 1 << 30, None)
-    assert rc == 2 and "forward workspace" in L.msa_last_error().decode()
+    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8,
+                   16, 16, 16, 16, 1, 16, 16, 16, 16, 16, 16, 10, None)
+    assert rc == 2 and "backward workspace" in L.msa_last_error().decode()
+    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8,
+                   16, 16, 16, 16, 0, 16, 16, 16, 16, 16, 16, 1 << 20, None)
+    assert rc == 2 and "tile_bits" in L.msa_last_error().decode()
     rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 0, 100, 16, 16,
                       1e-8, 16, 16, 1 << 30, None)
     assert rc == 1 and "cache_len" in L.msa_last_error().decode()

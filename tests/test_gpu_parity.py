@@ -31,11 +31,11 @@ def _rw(H, r, w):
             torch.tensor(w, dtype=torch.float32, device=DEV))
 
 
-def _run_fwd(q, k, v, r, w, causal=True, kpm=None, need_bwd=True):
+def _run_fwd(q, k, v, r, w, causal=True, kpm=None):
     ops = _ops()
     rg, wg = _rw(q.shape[2], r, w)
     out = ops.fwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), rg, wg, causal, 1e-8,
-                      None if kpm is None else kpm.to(DEV), need_bwd=need_bwd)
+                      None if kpm is None else kpm.to(DEV))
     torch.cuda.synchronize()
     return out
 
@@ -69,6 +69,9 @@ FWD_CASES = [
     (1, 70, 150, 2, 32, False, [1.1, 1.25], [20.0, 400.0], True),          # cross, Tq != Tk
     (1, 96, 96, 2, 128, True, [1.1, 1.2], [50.0, 96.0], False),
     (1, 257, 257, 3, 64, False, [1.12, 1.2, 1.5], [64.5, 129.0, 1e4], False),
+    # head_dim 32: the instantiation where an unguarded MFMA source-register
+    # hazard once corrupted dq/dk (see the guard in msa_device.h)
+    (1, 128, 128, 2, 32, True, [1.1, 1.25], [20.0, 400.0], False),
 ]
 
 
@@ -88,7 +91,7 @@ def _case_inputs(case, dtype, seed=0):
 def test_forward_parity(case, dtype):
     B, Tq, Tk, H, D, causal, r, w, use_kpm = case
     q, k, v, kpm = _case_inputs(case, dtype)
-    y, hnorm, bits, ws = _run_fwd(q, k, v, r, w, causal, kpm)
+    y, hnorm, bits = _run_fwd(q, k, v, r, w, causal, kpm)
     kpm_np = None if kpm is None else kpm.numpy()
     yref, href = O.forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), causal,
                            key_padding_mask=kpm_np, return_h=True)
@@ -109,8 +112,8 @@ def test_backward_parity(case, dtype):
     rg, wg = _rw(H, r, w)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     kpm_d = None if kpm is None else kpm.to(DEV)
-    y, hnorm, bits, ws = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, kpm_d, need_bwd=True)
-    dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, ws, dy.to(DEV))
+    y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, kpm_d)
+    dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dy.to(DEV), kpm_d)
     torch.cuda.synchronize()
     kpm_np = None if kpm is None else kpm.numpy()
     # the backward differentiates the kernel's own forward output y, so the
@@ -134,8 +137,8 @@ def test_backward_deterministic():
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     outs = []
     for _ in range(2):
-        y, hnorm, bits, ws = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None, need_bwd=True)
-        outs.append((y,) + ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, ws, dy))
+        y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None)
+        outs.append((y,) + ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dy))
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
@@ -145,7 +148,7 @@ def test_tile_bitmap_matches_oracle_counts():
     B, T, H, D = 1, 640, 4, 64
     q, k, v = correlated_qkv(B, T, T, H, D, seed=4, dtype=torch.float32, rho=0.3)
     r, w = [1.1, 1.3, 1.6, 2.0], [100.0, 250.5, 640.0, 1e5]
-    y, hnorm, bits, ws = _run_fwd(q, k, v, r, w, True)
+    y, hnorm, bits = _run_fwd(q, k, v, r, w, True)
     nW, nA, act = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True)
     nqt = nkt = T // 64
     words = (nkt + 31) // 32
@@ -220,7 +223,7 @@ def test_cfg2_full_size_sampled_rows_bf16():
     w = (256 + (8192 - 256) * torch.rand(H, generator=g)).tolist()
     # sharpen some heads so the sampled rows carry live pairs
     r[0], r[1] = 1.15, 1.3
-    y = _run_fwd(q, k, v, r, w, True, need_bwd=False)[0]
+    y = _run_fwd(q, k, v, r, w, True)[0]
     rows = [0, 1, 63, 64, 1000, 4095, 4096, 8191]
     yref = O.rows_forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), rows, True)
     assert np.max(np.abs(yref)) > 1e-3
