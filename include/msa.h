@@ -141,16 +141,17 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
 
 /* Kernel timing for measurement.  After msa_timer_arm(kernel, n) the next n
  * launches of that kernel (any entry point) each record a HIP event pair on
- * their stream around the launch; msa_timer_read waits for the recorded
- * pairs and writes their durations in milliseconds, returning how many were
- * recorded.  msa_timer_arm(0, 0) disarms.  Process-wide; not for concurrent
- * use from several threads. */
+ * their stream around the launch; several kernels can be armed at once.
+ * msa_timer_read(kernel, ...) waits for that kernel's recorded pairs and
+ * writes their durations in milliseconds, returning how many were recorded
+ * (-1 on error).  msa_timer_arm(0, 0) disarms every kernel.  Process-wide; not
+ * for concurrent use from several threads. */
 enum msa_kernel_id {
-  MSA_K_PREP_K = 1, MSA_K_FWD = 2, /* 3: unused */ MSA_K_DKDV = 4,
+  MSA_K_PREP_K = 1, MSA_K_FWD_SCREEN = 2, MSA_K_FWD_LIVE = 3, MSA_K_DKDV = 4,
   MSA_K_DQ = 5, MSA_K_RW_REDUCE = 6, MSA_K_DECODE = 7
 };
 int msa_timer_arm(int kernel, int n);
-int msa_timer_read(float* ms, int n);
+int msa_timer_read(int kernel, float* ms, int n);
 
 /* Device self-test of the MFMA operand layouts the kernels assume: writes the
  * 32x32 products A.B (bf16 32x32x16 and fp32 32x32x2 forms) of the given

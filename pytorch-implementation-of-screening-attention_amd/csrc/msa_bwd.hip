@@ -66,62 +66,40 @@ struct BwdKArgs {
   float eps;
 };
 
-// Query-side rows for row i of head (b,h): raw q with 1/|q|, and dh.
+// Query-side rows for row i of head (b,h): raw q with 1/|q|, and dh (rounded
+// to T, as the MFMA operand it becomes).  Rows past Tq read row 0 and are
+// zeroed.
 template <typename T, int DP>
-__device__ inline void query_rows(const BwdKArgs& a, int b, int h, int bh, int i, int half, Row<T, DP>& qr,
-                                  float& iq, Row<T, DP>& dh) {
+__device__ inline void query_rows(const BwdKArgs& a, int b, int h, int bh, int i, int half, PRow<T, DP>& qr,
+                                  float& iq, PRow<T, DP>& dh) {
   const bool ok = i < a.Tq;
   const int ii = ok ? i : 0;
-  qr.load((const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, ok, a.D, half);
-  iq = qr.inv_norm(a.eps);
   const int64_t yoff = (((int64_t)b * a.Tq + ii) * a.H + h) * a.D;
-  Row<T, DP> yr;
+  PRow<T, DP> yr;
+  qr.load((const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, ok, a.D, half);
   yr.load((const T*)a.y + yoff, ok, a.D, half);
   dh.load((const T*)a.dy + yoff, ok, a.D, half);
+  const float hn = a.hnorm[(int64_t)bh * a.Tq + ii];
+  iq = qr.inv_norm(a.eps);
   const float ydot = yr.dot(dh);
   float c1, c2;
-  tanhnorm_coefs(ok ? a.hnorm[(int64_t)bh * a.Tq + ii] : 0.0f, a.eps, c1, c2);
-  const float cy = c2 * ydot;
-#pragma unroll
-  for (int n = 0; n < Row<T, DP>::N; ++n) dh.x[n] = c1 * dh.x[n] + cy * yr.x[n];
+  tanhnorm_coefs(ok ? hn : 0.0f, a.eps, c1, c2);
+  dh.axpby(c1, c2 * ydot, yr);
 }
 
 // Key-side rows for key j of head (b,h): raw k with 1/|k| (0 for padded or
 // masked keys) and raw v with 1/|v|.
 template <typename T, int DP>
-__device__ inline void key_rows(const BwdKArgs& a, int b, int h, int j, int half, Row<T, DP>& kr, float& ik,
-                                Row<T, DP>& vr, float& iv) {
+__device__ inline void key_rows(const BwdKArgs& a, int b, int h, int j, int half, PRow<T, DP>& kr, float& ik,
+                                PRow<T, DP>& vr, float& iv) {
   const bool ok = j < a.Tk;
   const int jj = ok ? j : 0;
   kr.load((const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, ok, a.D, half);
   vr.load((const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, ok, a.D, half);
+  const bool masked = a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + jj] != 0;
   ik = kr.inv_norm(a.eps);
   iv = vr.inv_norm(a.eps);
-  if (!ok || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + jj])) ik = 0.0f;
-}
-
-// Writes the lane's slots of operand row `m` (rounded to T) into a transposed
-// LDS tile t[d][m] of pitch ld.
-template <typename T, int DP>
-__device__ inline void stash_transposed(T* t, int ld, int m, const Row<T, DP>& row, int half) {
-  constexpr int KS = Mma<T>::KS, PER = Mma<T>::PER, NKS = DP / KS;
-#pragma unroll
-  for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-    for (int e = 0; e < PER; ++e) t[(KS * ks + PER * half + e) * ld + m] = from_f<T>(row.x[ks * PER + e]);
-}
-
-// Scale factors of the 16 rows a lane's C-block registers cover:
-// register r -> row 16*(r/8) + 8*half + r%8 of a 32-row half tile.
-__device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]) {
-#pragma unroll
-  for (int g = 0; g < 2; ++g)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(sc + 16 * g + 8 * half + 4 * u);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[8 * g + 4 * u + e] = v[e];
-    }
+  if (!ok || masked) ik = 0.0f;
 }
 
 // Writes dx = normalise-backward(dx^, x) for one row held in C-layout
@@ -167,23 +145,41 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[NDH], const T* xrow, b
     }
 }
 
-template <typename T>
-struct LdsT {
-  static constexpr int LD = 32 + 16 / (int)sizeof(T);  // padded pitch of a transposed half tile
-};
-
-// One wave (64-thread block) per 64-key tile of head (b,h); lane -> key
-// j = k0 + 32*kh + l32.
+// Waves per SIMD the backward kernels are register-budgeted for: two (256
+// registers a lane) where the bf16 working set fits, else one.
 template <typename T, int DP>
-__global__ __launch_bounds__(64) void dkdv_kernel(BwdKArgs a) {
+constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
+
+// Column scan helper: bit (qt, kt) of the live-tile bitmap.
+__device__ inline bool tile_bit(const BwdKArgs& a, int bh, int qt, int kt) {
+  return (a.bits[((int64_t)bh * a.nqt + qt) * a.nkt_words + (kt >> 5)] >> (kt & 31)) & 1u;
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV.  256-thread block per 64-key tile of head (b,h); wave w works on the
+// quadrant (keys 32*kh .. +31, queries 32*qh .. +31) of every live query tile
+// in the key tile's bitmap column, kh = w%2, qh = w/2, so the two waves of a
+// key half accumulate over different query halves.  Lane -> key
+// j = k0 + 32*kh + l32 of the C blocks; registers -> queries.  All operands
+// come straight from global memory (no LDS staging): the transposed Q^T and
+// dH^T operands of the dK/dV products are formed by identity MFMAs.  At the
+// end the two waves of a key half exchange one accumulator through LDS: the
+// qh = 0 wave finishes dk, the qh = 1 wave finishes dv.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dkdv_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  constexpr int LD = LdsT<T>::LD;
-  __shared__ __attribute__((aligned(16))) T tq[DP * LD];   // raw q^T [d][i]
-  __shared__ __attribute__((aligned(16))) T th[DP * LD];   // dh^T    [d][i]
-  __shared__ __attribute__((aligned(16))) float sq[32];    // 1/|q_i|
-  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  // per wave: its own K, V operand fragments [2][NKS][64 lanes] during the
+  // tile loop, then (same bytes) its accumulator for the exchange [NDH][16][64]
+  constexpr int KVB = 2 * NKS * kWave * (int)sizeof(frag), REDB = NDH * 16 * kWave * (int)sizeof(float);
+  constexpr int WB = KVB > REDB ? KVB : REDB;
+  __shared__ __attribute__((aligned(16))) char smem[4 * WB];
+  __shared__ __attribute__((aligned(16))) float sq[4][32];  // per wave: 1/|q| of its query rows
+  __shared__ float rw[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, kh = w & 1, qh = w >> 1;
+  const int half = lane >> 5, l32 = lane & 31;
   int kt, bh;
   xcd_order(kt, bh);
   const int b = bh / a.H, h = bh % a.H;
@@ -191,193 +187,214 @@ __global__ __launch_bounds__(64) void dkdv_kernel(BwdKArgs a) {
   const bool causal = a.causal != 0;
   const int k0 = kt * kTile;
 
-  // own keys as raw B operands, with their 1/|k| and 1/|v|
-  frag kf[2][NKS], vf[2][NKS];
-  float ikl[2], ivl[2];
-#pragma unroll
-  for (int kh = 0; kh < 2; ++kh) {
-    Row<T, DP> kr, vr;
-    key_rows<T, DP>(a, b, h, k0 + 32 * kh + l32, half, kr, ikl[kh], vr, ivl[kh]);
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      kf[kh][ks] = kr.frag(ks, 1.0f);
-      vf[kh][ks] = vr.frag(ks, 1.0f);
-    }
-  }
-
-  f32x16 adv[NDH][2], adk[NDH][2];
-#pragma unroll
-  for (int dh_ = 0; dh_ < NDH; ++dh_)
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) { adv[dh_][kh][r] = 0.0f; adk[dh_][kh][r] = 0.0f; }
-  float dr_acc = 0.0f, dw_acc = 0.0f;
-
   const int64_t klast = k0 + 63 < a.Tk - 1 ? k0 + 63 : a.Tk - 1;
   int64_t ilo = causal ? (int64_t)k0 : (int64_t)k0 - hp.wc + 1;
   int64_t ihi = klast + hp.wc - 1;
   if (ilo < 0) ilo = 0;
   if (ihi > a.Tq - 1) ihi = a.Tq - 1;
   const int qt_lo = (int)(ilo / kTile), qt_hi = ihi >= ilo ? (int)(ihi / kTile) : qt_lo - 1;
-
-  for (int base = qt_lo; base <= qt_hi; base += kWave) {
+  bool any = false;
+  for (int base = qt_lo; base <= qt_hi && !any; base += kWave) {
     const int ql = base + lane;
-    bool bit = false;
-    if (ql <= qt_hi) bit = (a.bits[((int64_t)bh * a.nqt + ql) * a.nkt_words + (kt >> 5)] >> (kt & 31)) & 1u;
-    unsigned long long mask = __ballot(bit);
-    while (mask != 0ull) {
-      const int qt = base + __builtin_ctzll(mask);
-      mask &= mask - 1ull;
-      const int q0 = qt * kTile;
+    any = __ballot(ql <= qt_hi && tile_bit(a, bh, ql, kt)) != 0ull;
+  }
 
-      // one 32-row half of the query tile at a time
-      for (int qh = 0; qh < 2; ++qh) {
-        // rows i = q0 + 32*qh + perm_row(l32) as A operands; transposes and
-        // 1/|q| into LDS
-        frag qa[NKS], ha[NKS];
-        wave_lds_sync();
-        {
-          const int m = perm_row(l32);
-          Row<T, DP> qr, dr;
-          float iq;
-          query_rows<T, DP>(a, b, h, bh, q0 + 32 * qh + m, half, qr, iq, dr);
+  // own keys as raw B operands (lane -> key), kept in LDS, with 1/|k| (0 if
+  // padded or masked) and 1/|v|
+  const int j = k0 + 32 * kh + l32;
+  frag* kvl = reinterpret_cast<frag*>(smem + w * WB);
+  float ikl = 0.0f, ivl = 0.0f;
+  f32x16 acc_k[NDH], acc_v[NDH];
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            qa[ks] = qr.frag(ks, 1.0f);
-            ha[ks] = dr.frag(ks, 1.0f);
-          }
-          stash_transposed<T, DP>(tq, LD, m, qr, half);
-          stash_transposed<T, DP>(th, LD, m, dr, half);
-          if (half == 0) sq[m] = iq;
-        }
-        wave_lds_sync();
-        float isq[16];
-        read_row_scales(sq, half, isq);
+  for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { acc_k[dblk][r] = 0.0f; acc_v[dblk][r] = 0.0f; }
+  float dr_acc = 0.0f, dw_acc = 0.0f;
 
-        f32x16 s[2], dp[2];
+  if (any) {
+    {
+      PRow<T, DP> kr, vr;
+      key_rows<T, DP>(a, b, h, j, half, kr, ikl, vr, ivl);
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) { s[kh][r] = 0.0f; dp[kh][r] = 0.0f; }
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh) {
-            s[kh] = M::mma(qa[ks], kf[kh][ks], s[kh]);
-            dp[kh] = M::mma(ha[ks], vf[kh][ks], dp[kh]);
-          }
-        // P (into s) and ds/|q| (into dp); register r -> query
-        // q0 + 32qh + 16(r/8) + 8half + r%8, lane -> key k0 + 32kh + l32
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const int rel0 = (q0 + 32 * qh + 8 * half) - (k0 + 32 * kh + l32);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-            const float sv = s[kh][r] * isq[r] * ikl[kh];
-            const float av = trim(sv, hp.r);
-            const bool lv = av > 0.0f && in_window(dd, hp.wc, causal);
-            float p = 0.0f, ds = 0.0f;
-            if (__ballot(lv) != 0) {
-              if (lv) {
-                const float m = softmask(dd, hp.iw);
-                const float g = dp[kh][r] * ivl[kh];
-                p = av * av * m;
-                ds = 2.0f * av * hp.r * m * g;
-                dr_acc -= 2.0f * av * (1.0f - sv) * m * g;
-                dw_acc += av * av * g * softmask_dw(dd, hp.iw);
-              }
-            }
-            s[kh][r] = p;
-            dp[kh][r] = ds * isq[r];
-          }
-        }
-        // dv^T[d][j] += sum_i dh^T[d][i] P[i][j];  dk^T[d][j] += sum_i q^T[d][i] (ds/|q|)[i][j]
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int r0 = c * PER;
-          const int ioff = rowof(r0, half);
-#pragma unroll
-          for (int dh_ = 0; dh_ < NDH; ++dh_) {
-            const frag ht = M::load(&th[(32 * dh_ + l32) * LD + ioff]);
-            const frag qT = M::load(&tq[(32 * dh_ + l32) * LD + ioff]);
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-              adv[dh_][kh] = M::mma(ht, M::pack(s[kh], r0), adv[dh_][kh]);
-              adk[dh_][kh] = M::mma(qT, M::pack(dp[kh], r0), adk[dh_][kh]);
-            }
-          }
-        }
+      for (int ks = 0; ks < NKS; ++ks) {
+        kvl[ks * kWave + lane] = kr.f[ks];
+        kvl[(NKS + ks) * kWave + lane] = vr.f[ks];
       }
     }
+    frag id[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
+
+    for (int base = qt_lo; base <= qt_hi; base += kWave) {
+      const int ql = base + lane;
+      unsigned long long mask = __ballot(ql <= qt_hi && tile_bit(a, bh, ql, kt));
+      while (mask != 0ull) {
+        const int qt = base + __builtin_ctzll(mask);
+        mask &= mask - 1ull;
+        const int q0 = qt * kTile;
+
+        // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
+        const int m = perm_row(l32);
+        frag qa[NKS], ha[NKS];
+        float isq[16];
+        {
+          PRow<T, DP> qr, dhr;
+          float iq;
+          query_rows<T, DP>(a, b, h, bh, q0 + 32 * qh + m, half, qr, iq, dhr);
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            qa[ks] = qr.f[ks];
+            ha[ks] = dhr.f[ks];
+          }
+          wave_lds_sync();
+          if (half == 0) sq[w][m] = iq;
+          wave_lds_sync();
+          read_row_scales(sq[w], half, isq);
+        }
+
+        // S = Q K^T and dP = dH V^T (raw operands)
+        f32x16 s, dp;
+        {
+          frag kf[NKS], vf[NKS];
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            kf[ks] = kvl[ks * kWave + lane];
+            vf[ks] = kvl[(NKS + ks) * kWave + lane];
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            s = M::mma_ng(qa[ks], kf[ks], s);
+            dp = M::mma_ng(ha[ks], vf[ks], dp);
+          }
+          guard_frags(kf);
+          guard_frags(vf);
+        }
+
+        // register r -> query q0 + 32qh + rowof(r, half), lane -> key j
+        const int rel0 = (q0 + 32 * qh + 8 * half) - j;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dd = rel0 + 16 * (r >> 3) + (r & 7);
+          const float sv = s[r] * isq[r] * ikl;
+          const float av = trim(sv, hp.r);
+          const bool pos = av > 0.0f;
+          float p = 0.0f, ds = 0.0f;
+          if (__ballot(pos) != 0ull) {
+            if (pos && in_window(dd, hp.wc, causal)) {
+              const float mk = softmask(dd, hp.iw);
+              const float g = dp[r] * ivl;
+              p = av * av * mk;
+              ds = 2.0f * av * hp.r * mk * g;
+              dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
+              dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+            }
+          }
+          s[r] = p;
+          dp[r] = ds * isq[r];
+        }
+        // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
+        // with dH^T, Q^T from identity products (packed A operands)
+        frag pb[NC], db[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          pb[c] = M::pack(s, c * PER);
+          db[c] = M::pack(dp, c * PER);
+        }
+        {
+          frag ta[NDH * NC];
+          f32x16 tr[NDH];
+          transpose_rows<T, DP>(ha, id, tr);
+#pragma unroll
+          for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int dblk = 0; dblk < NDH; ++dblk) acc_v[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], acc_v[dblk]);
+          guard_frags(ta);
+          transpose_rows<T, DP>(qa, id, tr);
+#pragma unroll
+          for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int dblk = 0; dblk < NDH; ++dblk) acc_k[dblk] = M::mma_ng(ta[dblk * NC + c], db[c], acc_k[dblk]);
+          guard_frags(ta);
+        }
+        guard_frags(qa);
+        guard_frags(ha);
+        guard_frags(pb);
+        guard_frags(db);
+      }
+    }
+    guard_frags(id);
   }
 
-  // Epilogue: dk^ = 1/|k| sum_i (ds/|q|) q and dv^ = 1/|v| ... -> fold the key's
-  // own scale, then the normalisation backward; written to (B,Tk,H,D).
+  // exchange: the qh = 0 wave of each key half finishes dk, the qh = 1 wave dv
+  wave_lds_sync();
+  float* redw = reinterpret_cast<float*>(smem + w * WB);
 #pragma unroll
-  for (int kh = 0; kh < 2; ++kh) {
-    const int j = k0 + 32 * kh + l32;
-    const bool valid = j < a.Tk;
-    const int jj = valid ? j : 0;
-    f32x16 accs[NDH];
-    const int64_t orow = (((int64_t)b * a.Tk + jj) * a.H + h) * a.D;
+  for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
-    for (int dh_ = 0; dh_ < NDH; ++dh_) accs[dh_] = adk[dh_][kh];
-    write_norm_bwd<T, NDH>(accs, (const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, valid, a.D,
-                           a.eps, half, (T*)a.dk + orow);
-#pragma unroll
-    for (int dh_ = 0; dh_ < NDH; ++dh_) accs[dh_] = adv[dh_][kh];
-    write_norm_bwd<T, NDH>(accs, (const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, valid, a.D,
-                           a.eps, half, (T*)a.dv + orow);
-  }
+    for (int r = 0; r < 16; ++r) redw[(dblk * 16 + r) * kWave + lane] = qh == 0 ? acc_v[dblk][r] : acc_k[dblk][r];
   dr_acc = wave_sum(dr_acc);
   dw_acc = wave_sum(dw_acc);
-  if (lane == 0) {
+  if (lane == 0) { rw[0][w] = dr_acc; rw[1][w] = dw_acc; }
+  __syncthreads();
+  f32x16 fin[NDH];
+#pragma unroll
+  for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float other = reinterpret_cast<const float*>(smem + (w ^ 2) * WB)[(dblk * 16 + r) * kWave + lane];
+      fin[dblk][r] = qh == 0 ? acc_k[dblk][r] + other : other + acc_v[dblk][r];
+    }
+  const bool valid = j < a.Tk;
+  const int jj = valid ? j : 0;
+  const int64_t orow = (((int64_t)b * a.Tk + jj) * a.H + h) * a.D;
+  if (qh == 0)
+    write_norm_bwd<T, NDH>(fin, (const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, valid, a.D,
+                           a.eps, half, (T*)a.dk + orow);
+  else
+    write_norm_bwd<T, NDH>(fin, (const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, valid, a.D,
+                           a.eps, half, (T*)a.dv + orow);
+  if (tid == 0) {
     const int64_t nbh = (int64_t)a.B * a.H;
-    a.part[(int64_t)bh * a.nkt + kt] = dr_acc;
-    a.part[nbh * a.nkt + (int64_t)bh * a.nkt + kt] = dw_acc;
+    a.part[(int64_t)bh * a.nkt + kt] = (rw[0][0] + rw[0][1]) + (rw[0][2] + rw[0][3]);
+    a.part[nbh * a.nkt + (int64_t)bh * a.nkt + kt] = (rw[1][0] + rw[1][1]) + (rw[1][2] + rw[1][3]);
   }
 }
 
-// One wave (64-thread block) per 64-query tile of head (b,h); lane -> query
-// i = q0 + 32*qh + l32.
+// ---------------------------------------------------------------------------
+// dQ.  256-thread block per 64-query tile of head (b,h); wave w works on the
+// quadrant (queries 32*qh .. +31, keys 32*kh .. +31) of every live key tile in
+// the query tile's bitmap row, qh = w/2, kh = w%2.  Lane -> query
+// i = q0 + 32*qh + l32; registers -> keys.  K^T comes from an identity MFMA.
+// The kh = 1 wave hands its accumulator to the kh = 0 wave through LDS, which
+// finishes dq.
+// ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(64) void dq_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  constexpr int LD = LdsT<T>::LD;
-  __shared__ __attribute__((aligned(16))) T tk[DP * LD];   // raw k^T [d][j]
-  __shared__ __attribute__((aligned(16))) float sk[32];    // 1/|k_j| (0 if masked)
-  __shared__ __attribute__((aligned(16))) float sv[32];    // 1/|v_j|
-  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  __shared__ __attribute__((aligned(16))) float sk[4][32];   // per wave: 1/|k| (0 if masked)
+  __shared__ __attribute__((aligned(16))) float sv[4][32];   // per wave: 1/|v|
+  __shared__ __attribute__((aligned(16))) float red[2][NDH][16][kWave];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, kh = w & 1, qh = w >> 1;
+  const int half = lane >> 5, l32 = lane & 31;
   int qt, bh;
   xcd_order(qt, bh);
   const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
   const int q0 = qt * kTile;
-
-  frag qb[2][NKS], hb[2][NKS];
-  float iql[2];
-#pragma unroll
-  for (int qh = 0; qh < 2; ++qh) {
-    Row<T, DP> qr, dr;
-    query_rows<T, DP>(a, b, h, bh, q0 + 32 * qh + l32, half, qr, iql[qh], dr);
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      qb[qh][ks] = qr.frag(ks, 1.0f);
-      hb[qh][ks] = dr.frag(ks, 1.0f);
-    }
-  }
-  f32x16 adq[NDH][2];
-#pragma unroll
-  for (int dh_ = 0; dh_ < NDH; ++dh_)
-#pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) adq[dh_][qh][r] = 0.0f;
+  const int i = q0 + 32 * qh + l32;
 
   const int64_t qlast = q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1;
   int64_t jlo = (int64_t)q0 - hp.wc + 1;
@@ -386,93 +403,130 @@ __global__ __launch_bounds__(64) void dq_kernel(BwdKArgs a) {
   if (jhi > a.Tk - 1) jhi = a.Tk - 1;
   const int kt_lo = (int)(jlo / kTile), kt_hi = jhi >= jlo ? (int)(jhi / kTile) : kt_lo - 1;
   const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
-
-  for (int base = kt_lo; base <= kt_hi; base += kWave) {
+  bool any = false;
+  for (int base = kt_lo; base <= kt_hi && !any; base += kWave) {
     const int kl = base + lane;
-    const bool bit = kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u);
-    unsigned long long mask = __ballot(bit);
-    while (mask != 0ull) {
-      const int kt = base + __builtin_ctzll(mask);
-      mask &= mask - 1ull;
-      const int k0 = kt * kTile;
+    any = __ballot(kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u)) != 0ull;
+  }
 
-      // one 32-key half of the key tile at a time
-      for (int kh = 0; kh < 2; ++kh) {
-        // key rows j = k0 + 32*kh + perm_row(l32) as A operands; k^T and the
-        // key scales into LDS
+  f32x16 adq[NDH];
+#pragma unroll
+  for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
+
+  if (any) {
+    // own queries as raw B operands (lane -> query) and dh
+    frag qb[NKS], hb[NKS];
+    float iql;
+    {
+      PRow<T, DP> qr, dhr;
+      query_rows<T, DP>(a, b, h, bh, i, half, qr, iql, dhr);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        qb[ks] = qr.f[ks];
+        hb[ks] = dhr.f[ks];
+      }
+    }
+    frag id[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
+
+    for (int base = kt_lo; base <= kt_hi; base += kWave) {
+      const int kl = base + lane;
+      unsigned long long mask = __ballot(kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u));
+      while (mask != 0ull) {
+        const int kt = base + __builtin_ctzll(mask);
+        mask &= mask - 1ull;
+        const int k0 = kt * kTile;
+
+        // key rows j = k0 + 32*kh + perm_row(l32) as A operands
+        const int m = perm_row(l32);
         frag ka[NKS], va[NKS];
-        wave_lds_sync();
+        float isk[16], isv[16];
         {
-          const int m = perm_row(l32);
-          Row<T, DP> kr, vr;
+          PRow<T, DP> kr, vr;
           float ik, iv;
           key_rows<T, DP>(a, b, h, k0 + 32 * kh + m, half, kr, ik, vr, iv);
 #pragma unroll
           for (int ks = 0; ks < NKS; ++ks) {
-            ka[ks] = kr.frag(ks, 1.0f);
-            va[ks] = vr.frag(ks, 1.0f);
+            ka[ks] = kr.f[ks];
+            va[ks] = vr.f[ks];
           }
-          stash_transposed<T, DP>(tk, LD, m, kr, half);
-          if (half == 0) { sk[m] = ik; sv[m] = iv; }
+          wave_lds_sync();
+          if (half == 0) { sk[w][m] = ik; sv[w][m] = iv; }
+          wave_lds_sync();
+          read_row_scales(sk[w], half, isk);
+          read_row_scales(sv[w], half, isv);
         }
-        wave_lds_sync();
-        float isk[16], isv[16];
-        read_row_scales(sk, half, isk);
-        read_row_scales(sv, half, isv);
 
-        f32x16 s[2], dp[2];
+        // S^T = K Q^T, dP^T = V dH^T; K^T by identity, packed at once as the
+        // A operand of the dQ product
+        f32x16 s, dp;
+        frag kta[NDH * NC];
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
+        for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) { s[qh][r] = 0.0f; dp[qh][r] = 0.0f; }
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-          for (int qh = 0; qh < 2; ++qh) {
-            s[qh] = M::mma(ka[ks], qb[qh][ks], s[qh]);
-            dp[qh] = M::mma(va[ks], hb[qh][ks], dp[qh]);
-          }
-        // (ds/|k|)^T; register r -> key k0 + 32kh + 16(r/8) + 8half + r%8, lane -> query
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {
-          const int rel0 = (q0 + 32 * qh + l32) - (k0 + 32 * kh + 8 * half);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-            const float av = trim(s[qh][r] * isk[r] * iql[qh], hp.r);
-            const bool lv = av > 0.0f && in_window(dd, hp.wc, causal);
-            float ds = 0.0f;
-            if (__ballot(lv) != 0) {
-              if (lv) ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[qh][r] * isv[r];
-            }
-            dp[qh][r] = ds * isk[r];
-          }
+        for (int ks = 0; ks < NKS; ++ks) {
+          s = M::mma_ng(ka[ks], qb[ks], s);
+          dp = M::mma_ng(va[ks], hb[ks], dp);
         }
-        // dq^T[d][i] += sum_j k^T[d][j] (ds/|k|)^T[j][i]
+        {
+          f32x16 tr[NDH];
+          transpose_rows<T, DP>(ka, id, tr);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int r0 = c * PER;
-          const int koff = rowof(r0, half);
+          for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
-          for (int dh_ = 0; dh_ < NDH; ++dh_) {
-            const frag kT = M::load(&tk[(32 * dh_ + l32) * LD + koff]);
-#pragma unroll
-            for (int qh = 0; qh < 2; ++qh) adq[dh_][qh] = M::mma(kT, M::pack(dp[qh], r0), adq[dh_][qh]);
-          }
+            for (int c = 0; c < NC; ++c) kta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
         }
+        guard_frags(ka);
+        guard_frags(va);
+
+        // register r -> key k0 + 32kh + rowof(r, half), lane -> query i
+        const int rel0 = i - (k0 + 32 * kh + 8 * half);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+          const float av = trim(s[r] * isk[r] * iql, hp.r);
+          const bool pos = av > 0.0f;
+          float ds = 0.0f;
+          if (__ballot(pos) != 0ull) {
+            if (pos && in_window(dd, hp.wc, causal)) ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+          }
+          dp[r] = ds * isk[r];
+        }
+        // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
+        frag db[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int dblk = 0; dblk < NDH; ++dblk) adq[dblk] = M::mma_ng(kta[dblk * NC + c], db[c], adq[dblk]);
+        guard_frags(db);
+        guard_frags(kta);
       }
     }
+    guard_frags(qb);
+    guard_frags(hb);
+    guard_frags(id);
   }
 
+  if (kh == 1) {
 #pragma unroll
-  for (int qh = 0; qh < 2; ++qh) {
-    const int i = q0 + 32 * qh + l32;
+    for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[qh][dblk][r][lane] = adq[dblk][r];
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) adq[dblk][r] += red[qh][dblk][r][lane];
     const bool valid = i < a.Tq;
     const int ii = valid ? i : 0;
-    f32x16 accs[NDH];
-#pragma unroll
-    for (int dh_ = 0; dh_ < NDH; ++dh_) accs[dh_] = adq[dh_][qh];
-    write_norm_bwd<T, NDH>(accs, (const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, valid, a.D,
+    write_norm_bwd<T, NDH>(adq, (const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, valid, a.D,
                            a.eps, half, (T*)a.dq + (((int64_t)b * a.Tq + ii) * a.H + h) * a.D);
   }
 }
@@ -519,12 +573,12 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   ka.nqt = g.nqt; ka.nkt = g.nkt; ka.nkt_words = g.nkt_words; ka.causal = g.causal;
   ka.eps = c.eps;
   timer_begin(4, c.stream);
-  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)g.nkt, (unsigned)(g.B * g.H)), dim3(64), 0, c.stream, ka);
+  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)g.nkt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
   timer_end(4, c.stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(5, c.stream);
-  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(64), 0, c.stream, ka);
+  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
   timer_end(5, c.stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -74,15 +74,26 @@ int hip_status(hipError_t e, const char* what) {
   return ok();
 }
 
-struct TimerState {
-  std::mutex mu;
-  int kernel = 0;
+// One armed event list per kernel id; several kernels may be armed at once.
+struct TimerSlot {
   int next = 0;
   std::vector<hipEvent_t> start, stop;
+};
+struct TimerState {
+  std::mutex mu;
+  TimerSlot slot[MSA_K_DECODE + 1];
 };
 TimerState& timer() {
   static TimerState t;
   return t;
+}
+
+void timer_clear(TimerSlot& s) {
+  for (hipEvent_t e : s.start) (void)hipEventDestroy(e);
+  for (hipEvent_t e : s.stop) (void)hipEventDestroy(e);
+  s.start.clear();
+  s.stop.clear();
+  s.next = 0;
 }
 
 }  // namespace
@@ -91,12 +102,14 @@ namespace msa {
 void timer_begin(int kernel, hipStream_t s) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
-  if (t.kernel == kernel && t.next < (int)t.start.size()) (void)hipEventRecord(t.start[t.next], s);
+  TimerSlot& sl = t.slot[kernel];
+  if (sl.next < (int)sl.start.size()) (void)hipEventRecord(sl.start[sl.next], s);
 }
 void timer_end(int kernel, hipStream_t s) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
-  if (t.kernel == kernel && t.next < (int)t.stop.size()) (void)hipEventRecord(t.stop[t.next++], s);
+  TimerSlot& sl = t.slot[kernel];
+  if (sl.next < (int)sl.stop.size()) (void)hipEventRecord(sl.stop[sl.next++], s);
 }
 }  // namespace msa
 
@@ -105,32 +118,38 @@ extern "C" {
 int msa_timer_arm(int kernel, int n) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
-  for (hipEvent_t e : t.start) (void)hipEventDestroy(e);
-  for (hipEvent_t e : t.stop) (void)hipEventDestroy(e);
-  t.start.clear();
-  t.stop.clear();
-  t.kernel = 0;
-  t.next = 0;
-  if (kernel == 0 || n <= 0) return ok();
+  if (kernel == 0) {
+    for (TimerSlot& sl : t.slot) timer_clear(sl);
+    return ok();
+  }
   if (kernel < MSA_K_PREP_K || kernel > MSA_K_DECODE) return fail(MSA_ERR_INVALID, "unknown kernel id %d", kernel);
+  TimerSlot& sl = t.slot[kernel];
+  timer_clear(sl);
   for (int i = 0; i < n; ++i) {
     hipEvent_t a, b;
-    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
+    if (hipEventCreate(&a) != hipSuccess) return fail(MSA_ERR_HIP, "hipEventCreate failed");
+    if (hipEventCreate(&b) != hipSuccess) {
+      (void)hipEventDestroy(a);
       return fail(MSA_ERR_HIP, "hipEventCreate failed");
-    t.start.push_back(a);
-    t.stop.push_back(b);
+    }
+    sl.start.push_back(a);
+    sl.stop.push_back(b);
   }
-  t.kernel = kernel;
   return ok();
 }
 
-int msa_timer_read(float* ms, int n) {
+int msa_timer_read(int kernel, float* ms, int n) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
-  int cnt = t.next < n ? t.next : n;
+  if (kernel < MSA_K_PREP_K || kernel > MSA_K_DECODE) {
+    fail(MSA_ERR_INVALID, "unknown kernel id %d", kernel);
+    return -1;
+  }
+  TimerSlot& sl = t.slot[kernel];
+  int cnt = sl.next < n ? sl.next : n;
   for (int i = 0; i < cnt; ++i) {
-    if (hipEventSynchronize(t.stop[i]) != hipSuccess) return -1;
-    if (hipEventElapsedTime(&ms[i], t.start[i], t.stop[i]) != hipSuccess) return -1;
+    if (hipEventSynchronize(sl.stop[i]) != hipSuccess) return -1;
+    if (hipEventElapsedTime(&ms[i], sl.start[i], sl.stop[i]) != hipSuccess) return -1;
   }
   return cnt;
 }

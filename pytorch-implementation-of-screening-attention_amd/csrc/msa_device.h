@@ -42,6 +42,39 @@ template <typename F>
 __device__ inline void guard_mfma_sources(F& a, F& b) {
   asm volatile("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
 }
+// Group form: after a run of unguarded MFMAs (mma_ng), one s_nop block that
+// takes every A/B fragment of the run as a read-write operand.  The asm must
+// follow each MFMA that reads those registers (write-after-read order), so
+// none of them can be reused earlier than 16 wait states after the last one.
+#define MSA_NOP16 "s_nop 7\n\ts_nop 7"
+template <typename F>
+__device__ inline void guard_frags(F (&f)[2]) {
+  asm volatile(MSA_NOP16 : "+v"(f[0]), "+v"(f[1]));
+}
+template <typename F>
+__device__ inline void guard_frags(F (&f)[4]) {
+  asm volatile(MSA_NOP16 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+}
+template <typename F>
+__device__ inline void guard_frags(F (&f)[8]) {
+  asm volatile(MSA_NOP16 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]),
+               "+v"(f[7]));
+}
+template <typename F, int N>
+__device__ inline void guard_frags(F (&f)[N]) {
+  static_assert(N % 16 == 0, "guard_frags: unsupported fragment count");
+#pragma unroll
+  for (int c = 0; c < N; c += 16)
+    asm volatile(MSA_NOP16 : "+v"(f[c]), "+v"(f[c + 1]), "+v"(f[c + 2]), "+v"(f[c + 3]), "+v"(f[c + 4]),
+                 "+v"(f[c + 5]), "+v"(f[c + 6]), "+v"(f[c + 7]), "+v"(f[c + 8]), "+v"(f[c + 9]), "+v"(f[c + 10]),
+                 "+v"(f[c + 11]), "+v"(f[c + 12]), "+v"(f[c + 13]), "+v"(f[c + 14]), "+v"(f[c + 15]));
+}
+template <typename F>
+__device__ inline void guard_frags(F (&f)[16]) {
+  asm volatile(MSA_NOP16 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]),
+               "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]),
+               "+v"(f[14]), "+v"(f[15]));
+}
 
 template <> struct Mma<bf16> {
   static constexpr int KS = 16;
@@ -51,6 +84,10 @@ template <> struct Mma<bf16> {
     const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     guard_mfma_sources(a, b);
     return d;
+  }
+  // Unguarded: the caller guards every A/B fragment with guard_frags.
+  __device__ static inline f32x16 mma_ng(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
   __device__ static inline frag load(const bf16* p) { return *reinterpret_cast<const frag*>(p); }
   __device__ static inline frag zero() { frag z; for (int e = 0; e < 8; ++e) z[e] = (bf16)0.0f; return z; }
@@ -73,6 +110,9 @@ template <> struct Mma<float> {
     guard_mfma_sources(a, b);
     return d;
   }
+  __device__ static inline f32x16 mma_ng(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
   __device__ static inline frag load(const float* p) { return *p; }
   __device__ static inline frag zero() { return 0.0f; }
   __device__ static inline float get(const frag& f, int) { return f; }
@@ -90,6 +130,41 @@ __device__ inline int perm_row(int m) {
   return 16 * (g >> 1) + 8 * hh + 4 * (g & 1) + t;
 }
 __device__ inline int rowof(int r, int half) { return 16 * (r >> 3) + 8 * half + (r & 7); }
+
+// Transpose by MFMA.  For 32 rows X held as A fragments x[ks] (lane l%32 ->
+// row perm_row(l%32), slots -> columns d = KS*ks + PER*(l/32) + e), the product
+// X I with the identity gives, per 32-column block dblk, a C block with
+// lane -> column d = 32*dblk + l%32 and register r -> X row rowof(r, l/32).
+// Packed PER registers at a time, that is the A operand of a second product
+// that contracts over X's rows with a C block over the same rows (register
+// index = contraction index on both sides).  Products with 1 and sums with 0
+// are exact, so the values come through unchanged.
+// Slice c of the identity (k-step c of a 32-column block; it does not depend
+// on the block): slot e of lane l is 1 iff KS*c + PER*(l/32) + e == l%32.
+template <typename T>
+__device__ inline typename Mma<T>::frag ident_frag(int c, int lane) {
+  using M = Mma<T>;
+  const int l32 = lane & 31, half = lane >> 5;
+  f32x16 t;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) t[e] = (e < M::PER && M::KS * c + M::PER * half + e == l32) ? 1.0f : 0.0f;
+  return M::pack(t, 0);
+}
+// out[dblk] = (X I)[:, 32*dblk .. 32*dblk+31] with unguarded MFMAs: the
+// caller guards x and id (guard_frags) before they can be overwritten.
+template <typename T, int DP>
+__device__ inline void transpose_rows(const typename Mma<T>::frag (&x)[DP / Mma<T>::KS],
+                                      const typename Mma<T>::frag (&id)[32 / Mma<T>::KS], f32x16 (&out)[DP / 32]) {
+  using M = Mma<T>;
+  constexpr int NC = 32 / M::KS;
+#pragma unroll
+  for (int dblk = 0; dblk < DP / 32; ++dblk) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) out[dblk][r] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) out[dblk] = M::mma_ng(x[dblk * NC + c], id[c], out[dblk]);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Screening math for one (query i, key j) pair.
@@ -179,15 +254,22 @@ struct Row {
   static constexpr int KS = Mma<T>::KS, PER = Mma<T>::PER, NKS = DP / KS, N = NKS * PER;
   float x[N];
 
-  // Loads the lane's slots of row `p` (D valid columns); zeros when !ok.
+  // Loads the lane's slots of row `p` (D valid columns); zeros when !ok.  `p`
+  // must point at a readable row even when !ok (callers clamp the row index):
+  // every load is issued unconditionally and masked afterwards, so the loads
+  // of several rows can be in flight together.
   __device__ inline void load(const T* p, bool ok, int D, int half) {
+    typename Mma<T>::frag f[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int d0 = KS * ks + PER * half;
-      const bool in = ok && d0 < D;
-      const typename Mma<T>::frag f = in ? Mma<T>::load(p + d0) : Mma<T>::zero();
+      f[ks] = Mma<T>::load(p + (d0 < D ? d0 : 0));
+    }
 #pragma unroll
-      for (int e = 0; e < PER; ++e) x[ks * PER + e] = Mma<T>::get(f, e);
+    for (int ks = 0; ks < NKS; ++ks) {
+      const bool in = ok && KS * ks + PER * half < D;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[ks * PER + e] = in ? Mma<T>::get(f[ks], e) : 0.0f;
     }
   }
   // Full-row dot product with another row held by the same lanes.
@@ -206,6 +288,61 @@ struct Row {
     return Mma<T>::pack(t, 0);
   }
 };
+
+// An operand row kept in its storage type: the lane's NKS fragments (slots
+// d = KS*ks + PER*half + e), converted to fp32 only where arithmetic needs it.
+template <typename T, int DP>
+struct PRow {
+  using M = Mma<T>;
+  using frag = typename M::frag;
+  static constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS;
+  frag f[NKS];
+
+  // Same contract as Row::load: `p` readable even when !ok; unconditional
+  // loads, masked afterwards.
+  __device__ inline void load(const T* p, bool ok, int D, int half) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = KS * ks + PER * half;
+      f[ks] = M::load(p + (d0 < D ? d0 : 0));
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      if (!(ok && KS * ks + PER * half < D)) f[ks] = M::zero();
+  }
+  __device__ inline float dot(const PRow& o) const {
+    float s = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) s += M::get(f[ks], e) * M::get(o.f[ks], e);
+    return s + __shfl_xor(s, 32);
+  }
+  __device__ inline float inv_norm(float eps) const { return 1.0f / fmaxf(sqrtf(dot(*this)), eps); }
+  // this <- a*this + b*o, rounded to T
+  __device__ inline void axpby(float a, float b, const PRow& o) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      f32x16 t;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) t[e] = a * M::get(f[ks], e) + b * M::get(o.f[ks], e);
+      f[ks] = M::pack(t, 0);
+    }
+  }
+};
+
+// Scale factors of the 16 rows a lane's C-block registers cover:
+// register r -> row 16*(r/8) + 8*half + r%8 of a 32-row half tile.
+__device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]) {
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(sc + 16 * g + 8 * half + 4 * u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[8 * g + 4 * u + e] = v[e];
+    }
+}
 
 // Waits for this wave's LDS traffic and keeps the compiler from moving
 // memory operations across the point (LDS ops of one wave run in order).

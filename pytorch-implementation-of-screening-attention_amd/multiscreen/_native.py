@@ -14,7 +14,7 @@ MSA_F32 = 0
 MSA_BF16 = 1
 
 # kernel ids for msa_timer_arm (include/msa.h)
-K_PREP_K, K_FWD, K_DKDV, K_DQ, K_RW_REDUCE, K_DECODE = 1, 2, 4, 5, 6, 7
+K_PREP_K, K_FWD_SCREEN, K_FWD_LIVE, K_DKDV, K_DQ, K_RW_REDUCE, K_DECODE = 1, 2, 3, 4, 5, 6, 7
 
 _lock = threading.Lock()
 _lib = None
@@ -42,7 +42,7 @@ _SIGS = {
     "msa_decode": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                         _i, _i, _i, _i, _i, _i, _p, _p, _f, _p, _p, _sz, _p]),
     "msa_timer_arm": (_i, [_i, _i]),
-    "msa_timer_read": (_i, [ctypes.POINTER(ctypes.c_float), _i]),
+    "msa_timer_read": (_i, [_i, ctypes.POINTER(ctypes.c_float), _i]),
     "msa_selftest_mfma": (_i, [_p, _p, _p, _p, _p, _p, _p]),
 }
 
