@@ -27,6 +27,8 @@ struct PrepKArgs {
   const void* k; Strides3 ks;
   const uint8_t* kpm;
   void* khat;
+  uint32_t* bits;
+  int64_t bits_per_bh;  // bitmap words per (b, h)
   int H, Tk, D;
   int64_t Tk_pad;
   float eps;
@@ -60,6 +62,10 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
 #pragma unroll
     for (int e = 0; e < VEC; e += 4) store4(p + e, x[e] * inv, x[e + 1] * inv, x[e + 2] * inv, x[e + 3] * inv);
   }
+  // clear this head's live-tile bitmap rows; the screen ORs live bits in
+  uint32_t* brow = a.bits + (int64_t)bh * a.bits_per_bh;
+  for (int64_t wi = (int64_t)blockIdx.x * 256 + threadIdx.x; wi < a.bits_per_bh; wi += (int64_t)gridDim.x * 256)
+    brow[wi] = 0u;
 }
 
 struct FwdKArgs {
@@ -69,42 +75,10 @@ struct FwdKArgs {
   const float* r; const float* w;
   void* y; float* hnorm; uint32_t* bits;
   int H, Tq, Tk, D, nqt, nkt_words, causal;
+  int nsegl;  // screen blocks per 4-query-tile group (segment stride)
   int64_t Tk_pad;
   float eps;
 };
-
-// MFMAs of one 64x64 screen tile: acc[kh][qh] = K^ rows (A, permuted) x Q^T.
-// bf16: unguarded MFMAs plus one guard on the K fragments (the Q fragments
-// stay live and are guarded once after their last use); fp32: guarded MFMAs.
-template <typename T, int DP>
-__device__ inline void screen_mma(typename Mma<T>::frag (&kf)[2 * (DP / Mma<T>::KS)],
-                                  const typename Mma<T>::frag (&qf)[2 * (DP / Mma<T>::KS)], f32x16 (&acc)[2][2]) {
-  using M = Mma<T>;
-  constexpr int NKS = DP / M::KS;
-#pragma unroll
-  for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[kh][qh][r] = 0.0f;
-  if constexpr (sizeof(T) == 2) {
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
-          acc[kh][qh] = M::mma_ng(kf[kh * NKS + ks], qf[qh * NKS + ks], acc[kh][qh]);
-    guard_frags(kf);
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh) acc[kh][qh] = M::mma(kf[kh * NKS + ks], qf[qh * NKS + ks], acc[kh][qh]);
-  }
-}
 
 // Loads Q^T B-operand fragments (raw values) and 1/|q| for the 64 queries of
 // tile qt: lane -> query q0 + 32*qh + l32, slots -> d.
@@ -142,135 +116,203 @@ struct ScreenTile {
   static constexpr int TILEB = 64 * ROWB;            // bytes per staged key tile
   static constexpr int CPT = 64 * CPR / 256;         // DMA chunks per thread per tile
   static constexpr int NST = 4;                      // pipeline stages (3 tiles in flight)
+  static constexpr int SEG = 256;                    // key tiles per work segment
+  // LDS chunk position of global chunk c of row R: c ^ swz(R).  A ds_read_b128
+  // of 8 consecutive lanes touches rows base + {0..3, 8..11} (perm_row) at one
+  // chunk; swz makes those 8 reads hit distinct 16-byte bank groups.
+  __device__ static inline int swz(int R) {
+    if constexpr (CPR == 4) return ((R >> 1) & 1) | ((R >> 2) & 2);
+    else return (R & 3) | ((R >> 1) & 4);
+  }
 };
+constexpr int kScreenSegBlocks = 8;  // max blocks per query-tile group
 
 template <int N>
 __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
 
 // ---------------------------------------------------------------------------
 // Screen: 256-thread block = 4 waves, wave -> one 64-query tile of one head.
-// The block's key tiles stream through a 4-stage LDS ring filled by direct
-// global->LDS DMA three tiles ahead (no register staging, one raw barrier per
-// tile).  Chunks are XOR-swizzled within each key row so the A-operand reads
-// of 32 rows spread over the LDS banks.  Each wave forms S^T = K^ Q^T on MFMA
-// for the tiles of its own window and votes with a ballot whether any
-// in-window pair passes the trim-and-square threshold; the result is the
-// live-tile bitmap.
+// The key-tile range of the 4 tiles' windows is cut into segments of SEG
+// tiles; block x = (group, first segment) and the block steps through its
+// group's segments with stride nsegl, so the work per block stays bounded
+// whatever the window.  Within a segment the key tiles stream through a
+// 4-stage LDS ring filled by direct global->LDS DMA three tiles ahead (no
+// register staging, one raw barrier per tile).  Chunks are XOR-swizzled
+// within each key row so the A-operand reads spread over the LDS banks.  Each wave forms S^T = K^ Q^T on MFMA for the tiles of its own window
+// and votes with a ballot whether any in-window pair passes the
+// trim-and-square threshold; live bits are ORed into the bitmap (cleared by
+// prep_k_kernel), so segments that share a bitmap word need no ordering.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void fwd_screen_kernel(FwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   using G = ScreenTile<T, DP>;
-  constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS;
-  __shared__ __attribute__((aligned(16))) char ring[G::NST * G::TILEB];
+  constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NST = G::NST;
+  __shared__ __attribute__((aligned(16))) char ring[NST * G::TILEB];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
   const int half = lane >> 5, l32 = lane & 31;
   int bx, bh;
   xcd_order(bx, bh);
+  const int grp = bx / a.nsegl, seg0 = bx % a.nsegl;
   const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
-  const int qt = bx * 4 + wave;
+  const int qt = grp * 4 + wave;
   const bool wave_ok = qt < a.nqt;
   const int q0 = qt * kTile;
-
-  frag qf[2 * NKS];
-  float iq[2];
-  load_q_tile<T, DP>(a, b, h, q0, wave_ok, half, l32, qf, iq);
 
   int kt_lo, kt_hi, blo, bhi;
   key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
   if (!wave_ok) { kt_lo = 0; kt_hi = -1; }
   {
-    const int64_t bq0 = (int64_t)bx * 4 * kTile;
+    const int64_t bq0 = (int64_t)grp * 4 * kTile;
     key_tile_range(a, hp, causal, bq0, bq0 + 4 * kTile - 1 < a.Tq - 1 ? bq0 + 4 * kTile - 1 : a.Tq - 1, blo, bhi);
   }
+  if (blo + seg0 * G::SEG > bhi) return;  // block-uniform: no segment for this block
 
-  uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
-  if (wave_ok)
-    for (int wi = lane; wi < a.nkt_words; wi += kWave)
-      if (kt_hi < kt_lo || wi < (kt_lo >> 5) || wi > (kt_hi >> 5)) brow[wi] = 0u;
+  frag qf[2 * NKS];
+  float iq[2];
+  load_q_tile<T, DP>(a, b, h, q0, wave_ok, half, l32, qf, iq);
+  uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + (wave_ok ? qt : 0)) * a.nkt_words;
 
-  // DMA of key tile kt into ring slot kt % NST; LDS chunk position p of row r
-  // holds global chunk p ^ (r % CPR).
+  // DMA: chunk c = u*256 + tid of a tile (row c / CPR, LDS position c % CPR)
+  // comes from global chunk position ^ swz(row) of that row; the per-lane
+  // byte offset inside a tile is fixed, the tile base is uniform.
   const char* kg = (const char*)a.khat + (int64_t)bh * a.Tk_pad * G::ROWB;
-  auto issue = [&](int kt) {
-    char* slot = ring + (kt % G::NST) * G::TILEB;
+  uint32_t goff[G::CPT];
 #pragma unroll
-    for (int u = 0; u < G::CPT; ++u) {
-      const int c = u * 256 + tid;  // chunk position in the tile
-      const int row = c / G::CPR, p = c % G::CPR;
-      const char* src = kg + ((int64_t)kt * kTile + row) * G::ROWB + ((p ^ (row & (G::CPR - 1))) << 4);
-      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
-                                       (void __attribute__((address_space(3)))*)(slot + (u * 256 + wave * 64) * 16),
-                                       16, 0, 0);
+  for (int u = 0; u < G::CPT; ++u) {
+    const int c = u * 256 + tid;
+    const int row = c / G::CPR, p = c % G::CPR;
+    goff[u] = (uint32_t)(row * G::ROWB + ((p ^ G::swz(row)) << 4));
+  }
+  // ring slot of the n-th tile of a segment: n % NST
+  auto issue = [&](int kt, int slot_idx) {
+    const char* tb = kg + (int64_t)kt * G::TILEB;
+#pragma unroll
+    for (int u = 0; u < G::CPT; ++u)
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(tb + goff[u]),
+          (void __attribute__((address_space(3)))*)(ring + slot_idx * G::TILEB + (u * 256 + wave * 64) * 16), 16, 0,
+          0);
+  };
+  // A-operand rows of key half kh: row 32kh + perm_row(l32), 16-byte chunk
+  // (KS*ks + PER*half)*sizeof(T)/16 = ks*KS*sizeof(T)/16 + half*PER*sizeof(T)/16
+  uint32_t aoff[2][NKS];
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int R = 32 * kh + perm_row(l32);
+      const int byte = (KS * ks + PER * half) * (int)sizeof(T);
+      aoff[kh][ks] = (uint32_t)(R * G::ROWB + ((((byte >> 4) ^ G::swz(R)) << 4) | (byte & 15)));
+    }
+
+  // MFMAs of key half kh of the staged tile: acc[qh] = K^ rows 32kh + perm x Q^T
+  auto half_mma = [&](const char* slot, int kh, f32x16 (&acc)[2]) {
+    frag kf[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) kf[ks] = M::load((const T*)(slot + aoff[kh][ks]));
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[qh][r] = 0.0f;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma_ng(kf[ks], qf[qh * NKS + ks], acc[qh]);
+      guard_frags(kf);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma(kf[ks], qf[qh * NKS + ks], acc[qh]);
     }
   };
-  for (int kt = blo; kt <= bhi && kt < blo + G::NST - 1; ++kt) issue(kt);
-
-  // element d of row R of the staged tile in ring slot `slot`
-  auto lds_elem = [&](const char* slot, int R, int d) -> const T* {
-    const int byte = d * (int)sizeof(T);
-    return (const T*)(slot + R * G::ROWB + ((((byte >> 4) ^ (R & (G::CPR - 1))) << 4) | (byte & 15)));
+  // Threshold vote on key half kh of the tile at k0: a(s) is monotone in s and
+  // s = acc/|q_i| in acc, so the half has a live pair iff its largest
+  // in-window acc passes.  Register r of the half holds key
+  // k0 + 32kh + 16(r/8) + 8half + r%8.
+  auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh) -> bool {
+    const bool interior = causal ? (k0 + 63 <= q0 && q0 + 63 - k0 < hp.wc)
+                                 : (q0 + 63 - k0 < hp.wc && k0 + 63 - q0 < hp.wc);
+    bool lv = false;
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh) {
+      float mx = -INFINITY;
+      if (interior) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[qh][r]);
+      } else {
+        const int rel0 = (q0 + 32 * qh + l32) - k0 - 32 * kh - 8 * half;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+          if (in_window(dd, hp.wc, causal)) mx = fmaxf(mx, acc[qh][r]);
+        }
+      }
+      lv |= trim(mx * iq[qh], hp.r) > 0.0f;
+    }
+    return lv;
   };
 
-  uint32_t word = 0u;
-  for (int kt = blo; kt <= bhi; ++kt) {
-    // tile kt's DMA (own part) is complete when at most the younger tiles'
-    // chunks are outstanding; the barrier then covers all four waves
-    const int younger = bhi - kt < G::NST - 2 ? bhi - kt : G::NST - 2;
-    if (younger >= 2) wait_vmcnt<2 * G::CPT>();
-    else if (younger == 1) wait_vmcnt<G::CPT>();
-    else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    if (kt + G::NST - 1 <= bhi) issue(kt + G::NST - 1);
+  for (int sg = seg0;; sg += a.nsegl) {
+    const int slo = blo + sg * G::SEG;
+    if (slo > bhi) break;
+    const int shi = slo + G::SEG - 1 < bhi ? slo + G::SEG - 1 : bhi;
+#pragma unroll
+    for (int n = 0; n < NST - 1; ++n)
+      if (slo + n <= shi) issue(slo + n, n);
 
-    const bool mine = kt >= kt_lo && kt <= kt_hi;
-    bool live = false;
-    if (mine) {
-      const int k0 = kt * kTile;
-      const char* slot = ring + (kt % G::NST) * G::TILEB;
-      frag kf[2 * NKS];
+    // Software pipeline over the two 32-key halves of each tile: the vote on
+    // one half runs while the MFMAs of the next half are in flight.  Order in
+    // step kt: MFMA(kt, keys 0-31) -> finish tile kt-1 (vote on its keys
+    // 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).
+    uint32_t word = 0u;
+    f32x16 acc0[2], acc1[2];
+    bool pend = false, live0 = false;  // tile kt-1: keys 32-63 pending in acc1; vote on keys 0-31
+    int pk0 = 0;
+    auto finish = [&](int kd, bool lv) {
+      if (__ballot(lv) != 0) word |= 1u << (kd & 31);
+      if ((kd & 31) == 31 || kd == shi) {
+        if (word != 0u && lane == 0) atomicOr(&brow[kd >> 5], word);
+        word = 0u;
+      }
+    };
+    // unrolled by NST so every ring slot offset is a constant
+    for (int base = slo; base <= shi; base += NST) {
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-          kf[kh * NKS + ks] = M::load(lds_elem(slot, 32 * kh + perm_row(l32), KS * ks + PER * half));
-      f32x16 acc[2][2];
-      screen_mma<T, DP>(kf, qf, acc);
-      // Threshold vote: a(s) is monotone in s and s = acc/|q_i| in acc, so a
-      // tile has a live pair iff its largest in-window acc passes.
-      const bool interior = causal ? (k0 + 63 <= q0 && q0 + 63 - k0 < hp.wc)
-                                   : (q0 + 63 - k0 < hp.wc && k0 + 63 - q0 < hp.wc);
-#pragma unroll
-      for (int qh = 0; qh < 2; ++qh) {
-        float mx = -INFINITY;
-        if (interior) {
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[kh][qh][r]);
-        } else {
-          // register r of block kh holds key k0 + 32kh + 16(r/8) + 8half + r%8
-          const int rel0 = (q0 + 32 * qh + l32) - k0 - 8 * half;
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int dd = rel0 - (32 * kh + 16 * (r >> 3) + (r & 7));
-              if (in_window(dd, hp.wc, causal)) mx = fmaxf(mx, acc[kh][qh][r]);
-            }
+      for (int u = 0; u < NST; ++u) {
+        const int kt = base + u;
+        if (kt > shi) break;
+        // tile kt's DMA (own part) is complete when at most the younger
+        // tiles' chunks are outstanding; the barrier then covers all waves
+        const int younger = shi - kt < NST - 2 ? shi - kt : NST - 2;
+        if (younger >= 2) wait_vmcnt<2 * G::CPT>();
+        else if (younger == 1) wait_vmcnt<G::CPT>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + NST - 1 <= shi) issue(kt + NST - 1, (u + NST - 1) % NST);
+
+        const bool mine = kt >= kt_lo && kt <= kt_hi;
+        const char* slot = ring + u * G::TILEB;
+        if (mine) half_mma(slot, 0, acc0);
+        if (kt > slo) finish(kt - 1, pend && (live0 || vote_half(acc1, pk0, 1)));
+        if (mine) {
+          half_mma(slot, 1, acc1);
+          live0 = vote_half(acc0, kt * kTile, 0);
+          pk0 = kt * kTile;
         }
-        live |= trim(mx * iq[qh], hp.r) > 0.0f;
+        pend = mine;
       }
     }
-    if (__ballot(live) != 0) word |= 1u << (kt & 31);
-    if (mine && ((kt & 31) == 31 || kt == kt_hi)) {
-      if (lane == 0) brow[kt >> 5] = word;
-      word = 0u;
-    }
+    finish(shi, pend && (live0 || vote_half(acc1, pk0, 1)));
+    // every wave is done with the ring before the next segment refills it
+    __builtin_amdgcn_s_barrier();
   }
   guard_frags(qf);
 }
@@ -456,6 +498,7 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   if (g.Tk_pad > 0) {
     PrepKArgs pa;
     pa.k = c.k; pa.ks = c.ks; pa.kpm = c.kpm; pa.khat = c.khat;
+    pa.bits = c.bits; pa.bits_per_bh = (int64_t)g.nqt * g.nkt_words;
     pa.H = g.H; pa.Tk = g.Tk; pa.D = g.D; pa.Tk_pad = g.Tk_pad; pa.eps = c.eps;
     constexpr int RPB = 256 / (DP * (int)sizeof(T) / 16);
     timer_begin(1, c.stream);
@@ -470,9 +513,13 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   fa.r = c.r; fa.w = c.w; fa.y = c.y; fa.hnorm = c.hnorm; fa.bits = c.bits;
   fa.H = g.H; fa.Tq = g.Tq; fa.Tk = g.Tk; fa.D = g.D; fa.nqt = g.nqt; fa.nkt_words = g.nkt_words;
   fa.causal = g.causal; fa.Tk_pad = g.Tk_pad; fa.eps = c.eps;
+  {
+    const int nseg = (g.nkt + ScreenTile<T, DP>::SEG - 1) / ScreenTile<T, DP>::SEG;
+    fa.nsegl = nseg < kScreenSegBlocks ? (nseg > 0 ? nseg : 1) : kScreenSegBlocks;
+  }
   timer_begin(2, c.stream);
-  hipLaunchKernelGGL((fwd_screen_kernel<T, DP>), dim3((unsigned)((g.nqt + 3) / 4), (unsigned)(g.B * g.H)), dim3(256),
-                     0, c.stream, fa);
+  hipLaunchKernelGGL((fwd_screen_kernel<T, DP>), dim3((unsigned)((g.nqt + 3) / 4 * fa.nsegl), (unsigned)(g.B * g.H)),
+                     dim3(256), 0, c.stream, fa);
   timer_end(2, c.stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
