@@ -70,7 +70,9 @@ size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);
 
 /* Bytes of backward workspace: one (dr, dw) partial per (b, h, 64-key tile),
- * summed in a fixed order. */
+ * summed in a fixed order, plus dh = TanhNorm'(h)^T dy and 1/|q| per query
+ * row (padded to 64 rows per tile), which the dQ pass hands to the dK/dV
+ * pass. */
 size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
 /*

@@ -62,7 +62,9 @@ struct BwdKArgs {
   const float* r; const float* w;
   const uint32_t* bits;
   void* dq; void* dk; void* dv; float* part;
+  void* dh; float* iqs;  // workspace: dh [b*h][Tq_pad][DP] (T), 1/|q| [b*h][Tq_pad]
   int B, H, Tq, Tk, D, nqt, nkt, nkt_words, causal;
+  int64_t Tq_pad;
   float eps;
 };
 
@@ -150,35 +152,245 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[NDH], const T* xrow, b
 template <typename T, int DP>
 constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
 
-// Column scan helper: bit (qt, kt) of the live-tile bitmap.
-__device__ inline bool tile_bit(const BwdKArgs& a, int bh, int qt, int kt) {
-  return (a.bits[((int64_t)bh * a.nqt + qt) * a.nkt_words + (kt >> 5)] >> (kt & 31)) & 1u;
+// ---------------------------------------------------------------------------
+// dQ (runs first).  256-thread block per 64-query tile of head (b,h); wave w
+// works on the quadrant (queries 32*qh .. +31, keys 32*kh .. +31) of every
+// live key tile in the query tile's bitmap row, qh = w/2, kh = w%2.  Lane ->
+// query i = q0 + 32*qh + l32; registers -> keys.  The live key tiles' raw K
+// and V rows are staged into LDS by DMA, double-buffered: tile n+1 streams in
+// while tile n is computed.  K^T comes from an identity MFMA.  Side output for
+// dkdv_kernel: dh (rounded to T, as the operand it becomes) and 1/|q| of every
+// row of a query tile with a live key tile, in the workspace.  The kh = 1
+// wave hands its accumulator to the kh = 0 wave through LDS, which finishes dq.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
+  using M = Mma<T>;
+  using frag = typename M::frag;
+  using S = StageTile<T, DP>;
+  constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
+  __shared__ __attribute__((aligned(16))) char stage[2][2 * S::TILEB];  // [buffer][K tile | V tile]
+  __shared__ __attribute__((aligned(16))) float sk[4][32];              // per wave: 1/|k| (0 if masked)
+  __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v|
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
+  const int half = lane >> 5, l32 = lane & 31;
+  int qt, bh;
+  xcd_order(qt, bh);
+  const int b = bh / a.H, h = bh % a.H;
+  const HeadParams hp = head_params(a.r, a.w, h);
+  const bool causal = a.causal != 0;
+  const int q0 = qt * kTile;
+  const int i = q0 + 32 * qh + l32;
+  const bool valid = i < a.Tq;
+  const int ii = valid ? i : 0;
+  T* dqrow = (T*)a.dq + (((int64_t)b * a.Tq + ii) * a.H + h) * a.D;
+
+  const int64_t qlast = q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1;
+  int64_t jlo = (int64_t)q0 - hp.wc + 1;
+  int64_t jhi = causal ? qlast : qlast + hp.wc - 1;
+  if (jlo < 0) jlo = 0;
+  if (jhi > a.Tk - 1) jhi = a.Tk - 1;
+  const int kt_lo = (int)(jlo / kTile), kt_hi = jhi >= jlo ? (int)(jhi / kTile) : kt_lo - 1;
+  const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
+  auto bitf = [brow](int kl) { return ((brow[kl >> 5] >> (kl & 31)) & 1u) != 0u; };
+  BitWalk<decltype(bitf)> walk(bitf, kt_lo, kt_hi);
+  int cur = walk.next();
+  if (cur < 0) {  // block-uniform: no live key tile, dq = 0
+    if (kh == 0 && valid)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * dblk + 8 * g + 4 * half;
+          if (d < a.D) store4(dqrow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    return;
+  }
+
+  const T* krow0 = (const T*)a.k + b * a.ks.sb + h * a.ks.sh;
+  const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
+  const int m = perm_row(l32);
+  auto stage_tile = [&](int kt, int buf, uint8_t& msk) {
+    S::issue(krow0, a.ks.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf], tid, w);
+    S::issue(vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
+    const int j = kt * kTile + 32 * kh + m;
+    msk = (a.kpm != nullptr && j < a.Tk) ? a.kpm[(int64_t)b * a.Tk + j] : (uint8_t)0;
+  };
+  uint8_t mk_cur, mk_nxt = 0;
+  stage_tile(cur, 0, mk_cur);
+
+  // own queries as raw B operands (lane -> query) and dh, overlapping the DMA
+  frag qb[NKS], hb[NKS];
+  float iql;
+  {
+    PRow<T, DP> qr, dhr;
+    query_rows<T, DP>(a, b, h, bh, i, half, qr, iql, dhr);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      qb[ks] = qr.f[ks];
+      hb[ks] = dhr.f[ks];
+    }
+  }
+  if (kh == 0) {  // dh and 1/|q| of this tile's rows for dkdv_kernel (zero past Tq)
+    T* dst = (T*)a.dh + ((int64_t)bh * a.Tq_pad + i) * DP;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) *reinterpret_cast<frag*>(dst + KS * ks + PER * half) = hb[ks];
+    if (half == 0) a.iqs[(int64_t)bh * a.Tq_pad + i] = valid ? iql : 0.0f;
+  }
+  frag id[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
+  f32x16 adq[NDH];
+#pragma unroll
+  for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
+
+  int nxt = walk.next();
+  for (int it = 0; cur >= 0; ++it) {
+    wait_vmcnt<0>();
+    __syncthreads();  // tile `cur` is in LDS; the other buffer is free
+    if (nxt >= 0) stage_tile(nxt, (it + 1) & 1, mk_nxt);
+    const char* kl = stage[it & 1];
+    const char* vl = kl + S::TILEB;
+    const int k0 = cur * kTile;
+
+    // key rows j = k0 + 32*kh + perm_row(l32) as A operands, with 1/|k|
+    // (0 if padded or masked) and 1/|v|
+    const int j = k0 + 32 * kh + m;
+    const bool jok = j < a.Tk;
+    frag ka[NKS], va[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      ka[ks] = S::frag(kl, 32 * kh + m, ks, half, jok, a.D);
+      va[ks] = S::frag(vl, 32 * kh + m, ks, half, jok, a.D);
+    }
+    float isk[16], isv[16];
+    {
+      float s2k = 0.0f, s2v = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const float xk = M::get(ka[ks], e), xv = M::get(va[ks], e);
+          s2k += xk * xk;
+          s2v += xv * xv;
+        }
+      s2k += __shfl_xor(s2k, 32);
+      s2v += __shfl_xor(s2v, 32);
+      const float ik = (jok && mk_cur == 0) ? 1.0f / fmaxf(sqrtf(s2k), a.eps) : 0.0f;
+      const float iv = 1.0f / fmaxf(sqrtf(s2v), a.eps);
+      wave_lds_sync();
+      if (half == 0) { sk[w][m] = ik; sv[w][m] = iv; }
+      wave_lds_sync();
+      read_row_scales(sk[w], half, isk);
+      read_row_scales(sv[w], half, isv);
+    }
+
+    // S^T = K Q^T, dP^T = V dH^T; K^T by identity, packed at once as the A
+    // operand of the dQ product
+    f32x16 s, dp;
+    frag kta[NDH * NC];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      s = M::mma_ng(ka[ks], qb[ks], s);
+      dp = M::mma_ng(va[ks], hb[ks], dp);
+    }
+    {
+      f32x16 tr[NDH];
+      transpose_rows<T, DP>(ka, id, tr);
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+    }
+    guard_frags(ka);
+    guard_frags(va);
+
+    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i
+    const int rel0 = i - (k0 + 32 * kh + 8 * half);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+      const float av = trim(s[r] * isk[r] * iql, hp.r);
+      const bool pos = av > 0.0f;
+      float ds = 0.0f;
+      if (__ballot(pos) != 0ull) {
+        if (pos && valid && in_window(dd, hp.wc, causal)) ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+      }
+      dp[r] = ds * isk[r];
+    }
+    // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
+    frag db[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk) adq[dblk] = M::mma_ng(kta[dblk * NC + c], db[c], adq[dblk]);
+    guard_frags(db);
+    guard_frags(kta);
+
+    cur = nxt;
+    mk_cur = mk_nxt;
+    nxt = walk.next();
+  }
+  guard_frags(qb);
+  guard_frags(hb);
+  guard_frags(id);
+
+  // the kh = 1 wave's accumulator reaches the kh = 0 wave through the
+  // (now idle) stage buffers
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&stage[0][0]);  // [qh][NDH][16][64]
+  if (kh == 1) {
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((qh * NDH + dblk) * 16 + r) * kWave + lane] = adq[dblk][r];
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) adq[dblk][r] += red[((qh * NDH + dblk) * 16 + r) * kWave + lane];
+    write_norm_bwd<T, NDH>(adq, (const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, valid, a.D,
+                           a.eps, half, dqrow);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV.  256-thread block per 64-key tile of head (b,h); wave w works on the
-// quadrant (keys 32*kh .. +31, queries 32*qh .. +31) of every live query tile
-// in the key tile's bitmap column, kh = w%2, qh = w/2, so the two waves of a
-// key half accumulate over different query halves.  Lane -> key
-// j = k0 + 32*kh + l32 of the C blocks; registers -> queries.  All operands
-// come straight from global memory (no LDS staging): the transposed Q^T and
-// dH^T operands of the dK/dV products are formed by identity MFMAs.  At the
-// end the two waves of a key half exchange one accumulator through LDS: the
-// qh = 0 wave finishes dk, the qh = 1 wave finishes dv.
+// dK, dV (runs after dq_kernel).  256-thread block per 64-key tile of head
+// (b,h); wave w works on the quadrant (keys 32*kh .. +31, queries
+// 32*qh .. +31) of every live query tile in the key tile's bitmap column,
+// kh = w%2, qh = w/2, so the two waves of a key half accumulate over
+// different query halves.  Lane -> key j = k0 + 32*kh + l32 of the C blocks;
+// registers -> queries.  Per live query tile, its raw Q rows, the dh rows and
+// 1/|q| that dq_kernel left in the workspace are staged into LDS by DMA,
+// double-buffered.  The transposed Q^T and dH^T operands of the dK/dV products
+// are formed by identity MFMAs.  At the end the two waves of a key half
+// exchange one accumulator through LDS: the qh = 0 wave finishes dk, the
+// qh = 1 wave finishes dv.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dkdv_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
+  using S = StageTile<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  // per wave: its own K, V operand fragments [2][NKS][64 lanes] during the
-  // tile loop, then (same bytes) its accumulator for the exchange [NDH][16][64]
-  constexpr int KVB = 2 * NKS * kWave * (int)sizeof(frag), REDB = NDH * 16 * kWave * (int)sizeof(float);
-  constexpr int WB = KVB > REDB ? KVB : REDB;
-  __shared__ __attribute__((aligned(16))) char smem[4 * WB];
-  __shared__ __attribute__((aligned(16))) float sq[4][32];  // per wave: 1/|q| of its query rows
+  constexpr int SB = 2 * S::TILEB + 1024;  // per buffer: Q tile | dh tile | 1/|q| (64 floats, 1 KB slot)
+  constexpr int KVB = 2 * NKS * kWave * (int)sizeof(frag);  // per key half: own K, V fragments
+  constexpr int NBUF = 2 * SB + 2 * KVB <= 150 * 1024 ? 2 : 1;  // double-buffer where LDS allows
+  static_assert(4 * NDH * 16 * kWave * 4 <= NBUF * SB, "exchange must fit the stage buffers");
+  __shared__ __attribute__((aligned(16))) char stage[NBUF][SB];
+  __shared__ __attribute__((aligned(16))) char kvs[2][KVB];
   __shared__ float rw[2][4];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, kh = w & 1, qh = w >> 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
   const int half = lane >> 5, l32 = lane & 31;
   int kt, bh;
   xcd_order(kt, bh);
@@ -186,6 +398,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
   const int k0 = kt * kTile;
+  const int j = k0 + 32 * kh + l32;
+  const bool jvalid = j < a.Tk;
+  const int jj = jvalid ? j : 0;
+  const int64_t orow = (((int64_t)b * a.Tk + jj) * a.H + h) * a.D;
 
   const int64_t klast = k0 + 63 < a.Tk - 1 ? k0 + 63 : a.Tk - 1;
   int64_t ilo = causal ? (int64_t)k0 : (int64_t)k0 - hp.wc + 1;
@@ -193,155 +409,186 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   if (ilo < 0) ilo = 0;
   if (ihi > a.Tq - 1) ihi = a.Tq - 1;
   const int qt_lo = (int)(ilo / kTile), qt_hi = ihi >= ilo ? (int)(ihi / kTile) : qt_lo - 1;
-  bool any = false;
-  for (int base = qt_lo; base <= qt_hi && !any; base += kWave) {
-    const int ql = base + lane;
-    any = __ballot(ql <= qt_hi && tile_bit(a, bh, ql, kt)) != 0ull;
+  const uint32_t* bcol = a.bits + (int64_t)bh * a.nqt * a.nkt_words + (kt >> 5);
+  const int nw = a.nkt_words, sh = kt & 31;
+  auto bitf = [bcol, nw, sh](int ql) { return ((bcol[(int64_t)ql * nw] >> sh) & 1u) != 0u; };
+  BitWalk<decltype(bitf)> walk(bitf, qt_lo, qt_hi);
+  int cur = walk.next();
+  if (cur < 0) {  // block-uniform: no live query tile, dk = dv = 0
+    T* out = (T*)(qh == 0 ? a.dk : a.dv) + orow;
+    if (jvalid)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * dblk + 8 * g + 4 * half;
+          if (d < a.D) store4(out + d, 0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    if (tid == 0) {
+      const int64_t nbh = (int64_t)a.B * a.H;
+      a.part[(int64_t)bh * a.nkt + kt] = 0.0f;
+      a.part[nbh * a.nkt + (int64_t)bh * a.nkt + kt] = 0.0f;
+    }
+    return;
   }
 
-  // own keys as raw B operands (lane -> key), kept in LDS, with 1/|k| (0 if
-  // padded or masked) and 1/|v|
-  const int j = k0 + 32 * kh + l32;
-  frag* kvl = reinterpret_cast<frag*>(smem + w * WB);
-  float ikl = 0.0f, ivl = 0.0f;
+  const T* qrow0 = (const T*)a.q + b * a.qs.sb + h * a.qs.sh;
+  const T* dh0 = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
+  const float* iq0 = a.iqs + (int64_t)bh * a.Tq_pad;
+  auto stage_tile = [&](int qt, int buf) {
+    S::issue(qrow0, a.qs.st, (int64_t)qt * kTile, a.Tq, a.D, stage[buf], tid, w);
+    S::issue(dh0, DP, (int64_t)qt * kTile, a.Tq_pad, DP, stage[buf] + S::TILEB, tid, w);
+    if (w == 0)  // 64 floats of 1/|q|: lanes 0-15 carry them, the rest repeat lane 15 into the slot's tail
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(iq0 + (int64_t)qt * kTile + 4 * (lane < 16 ? lane : 15)),
+          (void __attribute__((address_space(3)))*)(stage[buf] + 2 * S::TILEB), 16, 0, 0);
+  };
+  stage_tile(cur, 0);
+
+  // own keys as raw B operands (lane -> key), kept in LDS (one copy per key
+  // half, written by its qh = 0 wave before the loop's first barrier), with
+  // 1/|k| (0 if padded or masked) and 1/|v|; overlapping the first DMA
+  frag* kvl = reinterpret_cast<frag*>(kvs[kh]);
+  float ikl, ivl;
+  {
+    PRow<T, DP> kr, vr;
+    key_rows<T, DP>(a, b, h, j, half, kr, ikl, vr, ivl);
+    if (qh == 0)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        kvl[ks * kWave + lane] = kr.f[ks];
+        kvl[(NKS + ks) * kWave + lane] = vr.f[ks];
+      }
+  }
+  frag id[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
   f32x16 acc_k[NDH], acc_v[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) { acc_k[dblk][r] = 0.0f; acc_v[dblk][r] = 0.0f; }
   float dr_acc = 0.0f, dw_acc = 0.0f;
+  const int m = perm_row(l32);
 
-  if (any) {
+  int nxt = walk.next();
+  for (int it = 0; cur >= 0; ++it) {
+    wait_vmcnt<0>();
+    __syncthreads();  // tile `cur` is in LDS; with two buffers the other one is free
+    if (NBUF == 2 && nxt >= 0) stage_tile(nxt, (it + 1) & 1);
+    const char* ql = stage[NBUF == 2 ? (it & 1) : 0];
+    const char* hl = ql + S::TILEB;
+    const float* iql = reinterpret_cast<const float*>(ql + 2 * S::TILEB);
+    const int q0 = cur * kTile;
+
+    // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
+    const bool iok = q0 + 32 * qh + m < a.Tq;
+    frag qa[NKS], ha[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      qa[ks] = S::frag(ql, 32 * qh + m, ks, half, iok, a.D);
+      ha[ks] = S::frag(hl, 32 * qh + m, ks, half, iok, DP);
+    }
+    float isq[16];
+    read_row_scales(iql + 32 * qh, half, isq);
+
+    // S = Q K^T and dP = dH V^T (raw operands)
+    f32x16 s, dp;
     {
-      PRow<T, DP> kr, vr;
-      key_rows<T, DP>(a, b, h, j, half, kr, ikl, vr, ivl);
+      frag kf[NKS], vf[NKS];
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        kvl[ks * kWave + lane] = kr.f[ks];
-        kvl[(NKS + ks) * kWave + lane] = vr.f[ks];
+        kf[ks] = kvl[ks * kWave + lane];
+        vf[ks] = kvl[(NKS + ks) * kWave + lane];
       }
-    }
-    frag id[NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
-
-    for (int base = qt_lo; base <= qt_hi; base += kWave) {
-      const int ql = base + lane;
-      unsigned long long mask = __ballot(ql <= qt_hi && tile_bit(a, bh, ql, kt));
-      while (mask != 0ull) {
-        const int qt = base + __builtin_ctzll(mask);
-        mask &= mask - 1ull;
-        const int q0 = qt * kTile;
-
-        // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
-        const int m = perm_row(l32);
-        frag qa[NKS], ha[NKS];
-        float isq[16];
-        {
-          PRow<T, DP> qr, dhr;
-          float iq;
-          query_rows<T, DP>(a, b, h, bh, q0 + 32 * qh + m, half, qr, iq, dhr);
+      for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            qa[ks] = qr.f[ks];
-            ha[ks] = dhr.f[ks];
-          }
-          wave_lds_sync();
-          if (half == 0) sq[w][m] = iq;
-          wave_lds_sync();
-          read_row_scales(sq[w], half, isq);
-        }
-
-        // S = Q K^T and dP = dH V^T (raw operands)
-        f32x16 s, dp;
-        {
-          frag kf[NKS], vf[NKS];
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            kf[ks] = kvl[ks * kWave + lane];
-            vf[ks] = kvl[(NKS + ks) * kWave + lane];
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            s = M::mma_ng(qa[ks], kf[ks], s);
-            dp = M::mma_ng(ha[ks], vf[ks], dp);
-          }
-          guard_frags(kf);
-          guard_frags(vf);
-        }
-
-        // register r -> query q0 + 32qh + rowof(r, half), lane -> key j
-        const int rel0 = (q0 + 32 * qh + 8 * half) - j;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-          const float sv = s[r] * isq[r] * ikl;
-          const float av = trim(sv, hp.r);
-          const bool pos = av > 0.0f;
-          float p = 0.0f, ds = 0.0f;
-          if (__ballot(pos) != 0ull) {
-            if (pos && in_window(dd, hp.wc, causal)) {
-              const float mk = softmask(dd, hp.iw);
-              const float g = dp[r] * ivl;
-              p = av * av * mk;
-              ds = 2.0f * av * hp.r * mk * g;
-              dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
-              dw_acc += av * av * g * softmask_dw(dd, hp.iw);
-            }
-          }
-          s[r] = p;
-          dp[r] = ds * isq[r];
-        }
-        // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
-        // with dH^T, Q^T from identity products (packed A operands)
-        frag pb[NC], db[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          pb[c] = M::pack(s, c * PER);
-          db[c] = M::pack(dp, c * PER);
-        }
-        {
-          frag ta[NDH * NC];
-          f32x16 tr[NDH];
-          transpose_rows<T, DP>(ha, id, tr);
-#pragma unroll
-          for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int dblk = 0; dblk < NDH; ++dblk) acc_v[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], acc_v[dblk]);
-          guard_frags(ta);
-          transpose_rows<T, DP>(qa, id, tr);
-#pragma unroll
-          for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int dblk = 0; dblk < NDH; ++dblk) acc_k[dblk] = M::mma_ng(ta[dblk * NC + c], db[c], acc_k[dblk]);
-          guard_frags(ta);
-        }
-        guard_frags(qa);
-        guard_frags(ha);
-        guard_frags(pb);
-        guard_frags(db);
+      for (int ks = 0; ks < NKS; ++ks) {
+        s = M::mma_ng(qa[ks], kf[ks], s);
+        dp = M::mma_ng(ha[ks], vf[ks], dp);
       }
+      guard_frags(kf);
+      guard_frags(vf);
     }
-    guard_frags(id);
+
+    // register r -> query q0 + 32qh + rowof(r, half), lane -> key j
+    const int rel0 = (q0 + 32 * qh + 8 * half) - j;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int dd = rel0 + 16 * (r >> 3) + (r & 7);
+      const float sv = s[r] * isq[r] * ikl;
+      const float av = trim(sv, hp.r);
+      const bool pos = av > 0.0f;
+      float p = 0.0f, ds = 0.0f;
+      if (__ballot(pos) != 0ull) {
+        if (pos && in_window(dd, hp.wc, causal)) {
+          const float mk = softmask(dd, hp.iw);
+          const float g = dp[r] * ivl;
+          p = av * av * mk;
+          ds = 2.0f * av * hp.r * mk * g;
+          dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
+          dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+        }
+      }
+      s[r] = p;
+      dp[r] = ds * isq[r];
+    }
+    // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
+    // with dH^T, Q^T from identity products (packed A operands)
+    frag pb[NC], db[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      pb[c] = M::pack(s, c * PER);
+      db[c] = M::pack(dp, c * PER);
+    }
+    {
+      frag ta[NDH * NC];
+      f32x16 tr[NDH];
+      transpose_rows<T, DP>(ha, id, tr);
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int dblk = 0; dblk < NDH; ++dblk) acc_v[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], acc_v[dblk]);
+      guard_frags(ta);
+      transpose_rows<T, DP>(qa, id, tr);
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int dblk = 0; dblk < NDH; ++dblk) acc_k[dblk] = M::mma_ng(ta[dblk * NC + c], db[c], acc_k[dblk]);
+      guard_frags(ta);
+    }
+    guard_frags(qa);
+    guard_frags(ha);
+    guard_frags(pb);
+    guard_frags(db);
+
+    if (NBUF == 1 && nxt >= 0) {
+      __syncthreads();  // every wave is done with the single buffer
+      stage_tile(nxt, 0);
+    }
+    cur = nxt;
+    nxt = walk.next();
   }
+  guard_frags(id);
 
-  // exchange: the qh = 0 wave of each key half finishes dk, the qh = 1 wave dv
-  wave_lds_sync();
-  float* redw = reinterpret_cast<float*>(smem + w * WB);
+  // exchange through the (now idle) stage buffers: the qh = 0 wave of each
+  // key half finishes dk, the qh = 1 wave dv
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&stage[0][0]);  // [4 waves][NDH][16][64]
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) redw[(dblk * 16 + r) * kWave + lane] = qh == 0 ? acc_v[dblk][r] : acc_k[dblk][r];
+    for (int r = 0; r < 16; ++r)
+      red[((w * NDH + dblk) * 16 + r) * kWave + lane] = qh == 0 ? acc_v[dblk][r] : acc_k[dblk][r];
   dr_acc = wave_sum(dr_acc);
   dw_acc = wave_sum(dw_acc);
   if (lane == 0) { rw[0][w] = dr_acc; rw[1][w] = dw_acc; }
@@ -351,183 +598,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float other = reinterpret_cast<const float*>(smem + (w ^ 2) * WB)[(dblk * 16 + r) * kWave + lane];
+      const float other = red[(((w ^ 2) * NDH + dblk) * 16 + r) * kWave + lane];
       fin[dblk][r] = qh == 0 ? acc_k[dblk][r] + other : other + acc_v[dblk][r];
     }
-  const bool valid = j < a.Tk;
-  const int jj = valid ? j : 0;
-  const int64_t orow = (((int64_t)b * a.Tk + jj) * a.H + h) * a.D;
   if (qh == 0)
-    write_norm_bwd<T, NDH>(fin, (const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, valid, a.D,
+    write_norm_bwd<T, NDH>(fin, (const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, jvalid, a.D,
                            a.eps, half, (T*)a.dk + orow);
   else
-    write_norm_bwd<T, NDH>(fin, (const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, valid, a.D,
+    write_norm_bwd<T, NDH>(fin, (const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, jvalid, a.D,
                            a.eps, half, (T*)a.dv + orow);
   if (tid == 0) {
     const int64_t nbh = (int64_t)a.B * a.H;
     a.part[(int64_t)bh * a.nkt + kt] = (rw[0][0] + rw[0][1]) + (rw[0][2] + rw[0][3]);
     a.part[nbh * a.nkt + (int64_t)bh * a.nkt + kt] = (rw[1][0] + rw[1][1]) + (rw[1][2] + rw[1][3]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dQ.  256-thread block per 64-query tile of head (b,h); wave w works on the
-// quadrant (queries 32*qh .. +31, keys 32*kh .. +31) of every live key tile in
-// the query tile's bitmap row, qh = w/2, kh = w%2.  Lane -> query
-// i = q0 + 32*qh + l32; registers -> keys.  K^T comes from an identity MFMA.
-// The kh = 1 wave hands its accumulator to the kh = 0 wave through LDS, which
-// finishes dq.
-// ---------------------------------------------------------------------------
-template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
-  using M = Mma<T>;
-  using frag = typename M::frag;
-  constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  __shared__ __attribute__((aligned(16))) float sk[4][32];   // per wave: 1/|k| (0 if masked)
-  __shared__ __attribute__((aligned(16))) float sv[4][32];   // per wave: 1/|v|
-  __shared__ __attribute__((aligned(16))) float red[2][NDH][16][kWave];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, kh = w & 1, qh = w >> 1;
-  const int half = lane >> 5, l32 = lane & 31;
-  int qt, bh;
-  xcd_order(qt, bh);
-  const int b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h);
-  const bool causal = a.causal != 0;
-  const int q0 = qt * kTile;
-  const int i = q0 + 32 * qh + l32;
-
-  const int64_t qlast = q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1;
-  int64_t jlo = (int64_t)q0 - hp.wc + 1;
-  int64_t jhi = causal ? qlast : qlast + hp.wc - 1;
-  if (jlo < 0) jlo = 0;
-  if (jhi > a.Tk - 1) jhi = a.Tk - 1;
-  const int kt_lo = (int)(jlo / kTile), kt_hi = jhi >= jlo ? (int)(jhi / kTile) : kt_lo - 1;
-  const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
-  bool any = false;
-  for (int base = kt_lo; base <= kt_hi && !any; base += kWave) {
-    const int kl = base + lane;
-    any = __ballot(kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u)) != 0ull;
-  }
-
-  f32x16 adq[NDH];
-#pragma unroll
-  for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
-
-  if (any) {
-    // own queries as raw B operands (lane -> query) and dh
-    frag qb[NKS], hb[NKS];
-    float iql;
-    {
-      PRow<T, DP> qr, dhr;
-      query_rows<T, DP>(a, b, h, bh, i, half, qr, iql, dhr);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        qb[ks] = qr.f[ks];
-        hb[ks] = dhr.f[ks];
-      }
-    }
-    frag id[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
-
-    for (int base = kt_lo; base <= kt_hi; base += kWave) {
-      const int kl = base + lane;
-      unsigned long long mask = __ballot(kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u));
-      while (mask != 0ull) {
-        const int kt = base + __builtin_ctzll(mask);
-        mask &= mask - 1ull;
-        const int k0 = kt * kTile;
-
-        // key rows j = k0 + 32*kh + perm_row(l32) as A operands
-        const int m = perm_row(l32);
-        frag ka[NKS], va[NKS];
-        float isk[16], isv[16];
-        {
-          PRow<T, DP> kr, vr;
-          float ik, iv;
-          key_rows<T, DP>(a, b, h, k0 + 32 * kh + m, half, kr, ik, vr, iv);
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            ka[ks] = kr.f[ks];
-            va[ks] = vr.f[ks];
-          }
-          wave_lds_sync();
-          if (half == 0) { sk[w][m] = ik; sv[w][m] = iv; }
-          wave_lds_sync();
-          read_row_scales(sk[w], half, isk);
-          read_row_scales(sv[w], half, isv);
-        }
-
-        // S^T = K Q^T, dP^T = V dH^T; K^T by identity, packed at once as the
-        // A operand of the dQ product
-        f32x16 s, dp;
-        frag kta[NDH * NC];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          s = M::mma_ng(ka[ks], qb[ks], s);
-          dp = M::mma_ng(va[ks], hb[ks], dp);
-        }
-        {
-          f32x16 tr[NDH];
-          transpose_rows<T, DP>(ka, id, tr);
-#pragma unroll
-          for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) kta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-        }
-        guard_frags(ka);
-        guard_frags(va);
-
-        // register r -> key k0 + 32kh + rowof(r, half), lane -> query i
-        const int rel0 = i - (k0 + 32 * kh + 8 * half);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-          const float av = trim(s[r] * isk[r] * iql, hp.r);
-          const bool pos = av > 0.0f;
-          float ds = 0.0f;
-          if (__ballot(pos) != 0ull) {
-            if (pos && in_window(dd, hp.wc, causal)) ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
-          }
-          dp[r] = ds * isk[r];
-        }
-        // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
-        frag db[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int dblk = 0; dblk < NDH; ++dblk) adq[dblk] = M::mma_ng(kta[dblk * NC + c], db[c], adq[dblk]);
-        guard_frags(db);
-        guard_frags(kta);
-      }
-    }
-    guard_frags(qb);
-    guard_frags(hb);
-    guard_frags(id);
-  }
-
-  if (kh == 1) {
-#pragma unroll
-    for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[qh][dblk][r][lane] = adq[dblk][r];
-  }
-  __syncthreads();
-  if (kh == 0) {
-#pragma unroll
-    for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) adq[dblk][r] += red[qh][dblk][r][lane];
-    const bool valid = i < a.Tq;
-    const int ii = valid ? i : 0;
-    write_norm_bwd<T, NDH>(adq, (const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, valid, a.D,
-                           a.eps, half, (T*)a.dq + (((int64_t)b * a.Tq + ii) * a.H + h) * a.D);
   }
 }
 
@@ -557,8 +640,13 @@ __global__ __launch_bounds__(256) void rw_reduce_kernel(const float* part, float
   if (threadIdx.x == 0) { dr[h] = sr[0]; dw[h] = sw[0]; }
 }
 
+// Workspace: [dr/dw partials][dh][1/|q|], each 256-byte aligned.
+static int64_t bwd_part_bytes(const Geometry& g) { return round_up((int64_t)2 * g.B * g.H * g.nkt * 4, 256); }
+static int64_t bwd_dh_bytes(const Geometry& g) {
+  return round_up((int64_t)g.B * g.H * g.Tq_pad * g.DP * (int64_t)g.esize, 256);
+}
 size_t bwd_ws_bytes(const Geometry& g) {
-  return round_up((int64_t)2 * g.B * g.H * g.nkt * (int64_t)sizeof(float), 256);
+  return bwd_part_bytes(g) + bwd_dh_bytes(g) + round_up((int64_t)g.B * g.H * g.Tq_pad * 4, 256);
 }
 
 template <typename T, int DP>
@@ -568,22 +656,27 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   ka.q = c.q; ka.qs = c.qs; ka.k = c.k; ka.ks = c.ks; ka.v = c.v; ka.vs = c.vs; ka.kpm = c.kpm;
   ka.y = c.y; ka.dy = c.dy; ka.hnorm = c.hnorm;
   ka.r = c.r; ka.w = c.w; ka.bits = c.bits;
-  ka.dq = c.dq; ka.dk = c.dk; ka.dv = c.dv; ka.part = c.part;
+  ka.dq = c.dq; ka.dk = c.dk; ka.dv = c.dv;
+  char* ws = (char*)c.workspace;
+  ka.part = (float*)ws;
+  ka.dh = ws + bwd_part_bytes(g);
+  ka.iqs = (float*)(ws + bwd_part_bytes(g) + bwd_dh_bytes(g));
   ka.B = g.B; ka.H = g.H; ka.Tq = g.Tq; ka.Tk = g.Tk; ka.D = g.D;
   ka.nqt = g.nqt; ka.nkt = g.nkt; ka.nkt_words = g.nkt_words; ka.causal = g.causal;
+  ka.Tq_pad = g.Tq_pad;
   ka.eps = c.eps;
-  timer_begin(4, c.stream);
-  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)g.nkt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
-  timer_end(4, c.stream);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   timer_begin(5, c.stream);
   hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
   timer_end(5, c.stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  timer_begin(4, c.stream);
+  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)g.nkt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
+  timer_end(4, c.stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(6, c.stream);
-  hipLaunchKernelGGL(rw_reduce_kernel, dim3((unsigned)g.H), dim3(256), 0, c.stream, (const float*)c.part, c.dr, c.dw,
+  hipLaunchKernelGGL(rw_reduce_kernel, dim3((unsigned)g.H), dim3(256), 0, c.stream, (const float*)ka.part, c.dr, c.dw,
                      g.B, g.H, g.nkt);
   timer_end(6, c.stream);
   return hipGetLastError();

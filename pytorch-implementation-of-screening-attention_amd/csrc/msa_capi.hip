@@ -254,7 +254,7 @@ int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
   c.v = v; c.vs = {v_sb, v_st, v_sh};
   c.r = r; c.w = w; c.kpm = key_padding_mask; c.eps = eps;
   c.y = y; c.hnorm = hnorm; c.dy = dy; c.bits = tile_bits;
-  c.part = (float*)workspace;
+  c.workspace = workspace;
   c.dq = dq; c.dk = dk; c.dv = dv; c.dr = dr; c.dw = dw;
   c.stream = (hipStream_t)stream;
   return hip_status(msa::launch_bwd(c), "msa_bwd launch");

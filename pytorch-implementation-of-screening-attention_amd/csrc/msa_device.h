@@ -344,9 +344,91 @@ __device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]
     }
 }
 
+// Waits until at most N of this wave's vector memory operations (loads,
+// stores and global->LDS DMA) are outstanding.
+template <int N>
+__device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
+
 // Waits for this wave's LDS traffic and keeps the compiler from moving
 // memory operations across the point (LDS ops of one wave run in order).
 __device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// ---------------------------------------------------------------------------
+// 64-row tiles staged global -> LDS by direct DMA (global_load_lds, 16 bytes a
+// lane, no register round trip) for a 256-thread block.  LDS tile: 64 rows of
+// DP elements, row-major, with the 16-byte chunks of row R XOR-swizzled by
+// swz(R) so that the A-operand reads of 8 consecutive lanes (rows
+// base + {0..3, 8..11} under perm_row) fall in distinct bank groups.
+// Rows past the tensor's end read its last row and columns past D read the
+// row's first chunk (valid memory either way); consumers mask both.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+struct StageTile {
+  static constexpr int ROWB = DP * (int)sizeof(T);  // bytes per row
+  static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row (4..32)
+  static constexpr int TILEB = 64 * ROWB;           // bytes per tile
+  static constexpr int CPT = 64 * CPR / 256;        // chunks per thread
+  __device__ static inline int swz(int R) {
+    if constexpr (CPR == 4) return ((R >> 1) & 1) | ((R >> 2) & 2);
+    else return (R & 3) | ((R >> 1) & 4);
+  }
+  // byte offset of element d of row R
+  __device__ static inline int off(int R, int d) {
+    const int byte = d * (int)sizeof(T);
+    return R * ROWB + ((((byte >> 4) ^ swz(R)) << 4) | (byte & 15));
+  }
+  // DMA rows r0 .. r0+63 of a tensor whose row r starts at row0 + r*st
+  // (elements; nrows >= 1 rows, D valid columns) into `lds`.  `wave` must be
+  // wave-uniform (the LDS destination of one instruction is a uniform base).
+  __device__ static inline void issue(const T* row0, int64_t st, int64_t r0, int64_t nrows, int D, char* lds,
+                                      int tid, int wave) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = u * 256 + tid;
+      const int R = c / CPR, p = c % CPR;
+      int64_t row = r0 + R;
+      if (row > nrows - 1) row = nrows - 1;
+      int col = ((p ^ swz(R)) * 16) / (int)sizeof(T);
+      if (col >= D) col = 0;
+      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(row0 + row * st + col),
+                                       (void __attribute__((address_space(3)))*)(lds + (u * 256 + wave * 64) * 16),
+                                       16, 0, 0);
+    }
+  }
+  // A/B operand fragment: row R, slots d = KS*ks + PER*half + e; zero when
+  // the row is invalid or the slots lie past D.
+  __device__ static inline typename Mma<T>::frag frag(const char* lds, int R, int ks, int half, bool row_ok, int D) {
+    const int d0 = Mma<T>::KS * ks + Mma<T>::PER * half;
+    const typename Mma<T>::frag f = Mma<T>::load((const T*)(lds + off(R, d0)));
+    return (row_ok && d0 < D) ? f : Mma<T>::zero();
+  }
+};
+
+// Set bits of a sequence of bitmap positions lo..hi, visited in increasing
+// order 64 at a time through a wave ballot; bit(p) reads position p.  All
+// state is wave-uniform.
+template <typename F>
+struct BitWalk {
+  F bit;
+  int base, hi;
+  unsigned long long mask;
+  __device__ BitWalk(F f, int lo, int hi_) : bit(f), base(lo), hi(hi_) {
+    const int p = base + (int)(threadIdx.x & 63);
+    mask = __ballot(p <= hi && bit(p));
+  }
+  // next set position, or -1
+  __device__ inline int next() {
+    while (mask == 0ull) {
+      base += 64;
+      if (base > hi) return -1;
+      const int p = base + (int)(threadIdx.x & 63);
+      mask = __ballot(p <= hi && bit(p));
+    }
+    const int idx = base + __builtin_ctzll(mask);
+    mask &= mask - 1ull;
+    return idx;
+  }
+};
 
 // XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs
 // in linear order (x fastest); when the grid divides evenly, remap so each

@@ -127,9 +127,6 @@ struct ScreenTile {
 };
 constexpr int kScreenSegBlocks = 8;  // max blocks per query-tile group
 
-template <int N>
-__device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
-
 // ---------------------------------------------------------------------------
 // Screen: 256-thread block = 4 waves, wave -> one 64-query tile of one head.
 // The key-tile range of the 4 tiles' windows is cut into segments of SEG
@@ -321,22 +318,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // Live tiles.  256-thread block per 64-query tile; wave w works on the
 // quadrant (queries 32*qh .. +31, keys 32*kh .. +31) of every key tile the
 // screen marked live, qh = w/2, kh = w%2.  Lane -> query i = q0 + 32*qh + l32,
-// registers -> keys.  Per tile: S^T from K^ (the screen's operands, so the same
-// values), alpha*m (attention.py:92-119) with 1/|v_j| folded in, and
+// registers -> keys.  The live key tiles' K^ rows (workspace) and raw V rows
+// are staged into LDS by DMA, double-buffered: tile n+1 streams in while tile
+// n is computed.  Per tile: S^T from K^ (the screen's operands and order, so
+// the same values), alpha*m (attention.py:92-119) with 1/|v_j| folded in, and
 // H^T += V^T P^T with V^T from an identity MFMA on the raw V rows.  The kh = 1
 // wave hands its H^T to the kh = 0 wave through LDS, which applies TanhNorm
-// (norm.py:23-25) and writes y in (B,T,H,D) and |h| per row.  Rows with no live
-// tile get y = 0, |h| = 0.
+// (norm.py:23-25) and writes y in (B,T,H,D) and |h| per row.  Rows with no
+// live tile get y = 0, |h| = 0.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 2 : 1)))
 void fwd_live_kernel(FwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
+  using S = StageTile<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  __shared__ __attribute__((aligned(16))) float sv[4][32];  // per wave: 1/|v_j| of its key rows
-  __shared__ __attribute__((aligned(16))) float red[2][NDH][16][kWave];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, kh = w & 1, qh = w >> 1;
+  __shared__ __attribute__((aligned(16))) char stage[2][2 * S::TILEB];  // [buffer][K^ tile | V tile]
+  __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v_j| of its key rows
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
   const int half = lane >> 5, l32 = lane & 31;
   int qt, bh;
   xcd_order(qt, bh);
@@ -345,124 +346,162 @@ void fwd_live_kernel(FwdKArgs a) {
   const bool causal = a.causal != 0;
   const int q0 = qt * kTile;
   const int i = q0 + 32 * qh + l32;
+  const bool valid = i < a.Tq;
+  T* yrow = (T*)a.y + (((int64_t)b * a.Tq + (valid ? i : 0)) * a.H + h) * a.D;
 
   int kt_lo, kt_hi;
   key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
   const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
-  bool any = false;
-  for (int base = kt_lo; base <= kt_hi && !any; base += kWave) {
-    const int kl = base + lane;
-    any = __ballot(kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u)) != 0ull;
+  auto bitf = [brow](int kl) { return ((brow[kl >> 5] >> (kl & 31)) & 1u) != 0u; };
+  BitWalk<decltype(bitf)> walk(bitf, kt_lo, kt_hi);
+  int cur = walk.next();
+  if (cur < 0) {  // block-uniform: no live key tile, y = 0 and |h| = 0
+    if (kh == 0 && valid) {
+      if (half == 0) a.hnorm[(int64_t)bh * a.Tq + i] = 0.0f;
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * dblk + 8 * g + 4 * half;
+          if (d < a.D) store4(yrow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    return;
   }
 
+  const T* kg = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
+  const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
+  auto stage_tile = [&](int kt, int buf) {
+    S::issue(kg, DP, (int64_t)kt * kTile, a.Tk_pad, DP, stage[buf], tid, w);
+    S::issue(vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
+  };
+  stage_tile(cur, 0);
+
+  // own queries as raw B operands (lane -> query) and 1/|q_i|, overlapping the DMA
+  frag qf[NKS];
+  float iq;
+  {
+    PRow<T, DP> qr;
+    qr.load((const T*)a.q + b * a.qs.sb + (int64_t)(valid ? i : 0) * a.qs.st + h * a.qs.sh, valid, a.D, half);
+    iq = qr.inv_norm(a.eps);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
+  }
+  frag id[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
   f32x16 o[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dblk][r] = 0.0f;
+  const int m = perm_row(l32);
 
-  if (any) {
-    // own queries as raw B operands (lane -> query) and 1/|q_i|
-    frag qf[NKS];
-    float iq;
+  int nxt = walk.next();
+  for (int it = 0; cur >= 0; ++it) {
+    wait_vmcnt<0>();
+    __syncthreads();  // tile `cur` is in LDS; the other buffer is free
+    if (nxt >= 0) stage_tile(nxt, (it + 1) & 1);
+    const char* kl = stage[it & 1];
+    const char* vl = kl + S::TILEB;
+    const int k0 = cur * kTile;
+
+    // key rows j = k0 + 32*kh + perm_row(l32): K^ (zero past Tk) and raw V
+    // with 1/|v|
+    const int j = k0 + 32 * kh + m;
+    const bool jok = j < a.Tk;
+    frag kf[NKS], va[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      kf[ks] = S::frag(kl, 32 * kh + m, ks, half, true, DP);
+      va[ks] = S::frag(vl, 32 * kh + m, ks, half, jok, a.D);
+    }
+    float isv[16];
     {
-      const bool ok = i < a.Tq;
-      PRow<T, DP> qr;
-      qr.load((const T*)a.q + b * a.qs.sb + (int64_t)(ok ? i : 0) * a.qs.st + h * a.qs.sh, ok, a.D, half);
-      iq = qr.inv_norm(a.eps);
+      float s2 = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const float x = M::get(va[ks], e);
+          s2 += x * x;
+        }
+      s2 += __shfl_xor(s2, 32);
+      const float iv = 1.0f / fmaxf(sqrtf(s2), a.eps);
+      wave_lds_sync();
+      if (half == 0) sv[w][m] = iv;
+      wave_lds_sync();
+      read_row_scales(sv[w], half, isv);
     }
-    frag id[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
-    const T* kg = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
 
-    for (int base = kt_lo; base <= kt_hi; base += kWave) {
-      const int kl = base + lane;
-      unsigned long long mask = __ballot(kl <= kt_hi && ((brow[kl >> 5] >> (kl & 31)) & 1u));
-      while (mask != 0ull) {
-        const int kt = base + __builtin_ctzll(mask);
-        mask &= mask - 1ull;
-        const int k0 = kt * kTile;
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(kf[ks], qf[ks], s);
+      guard_frags(kf);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s = M::mma(kf[ks], qf[ks], s);
+    }
 
-        // key rows j = k0 + 32*kh + perm_row(l32): K^ (padded rows are zero
-        // and inside the buffer) and raw V with 1/|v|
-        const int m = perm_row(l32);
-        const int j = k0 + 32 * kh + m;
-        frag kf[NKS];
+    // P^T[j][i] = alpha_ij m_ij / |v_j|; register r -> key
+    // k0 + 32kh + rowof(r, half), lane -> query i
+    const int rel0 = i - (k0 + 32 * kh + 8 * half);
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) kf[ks] = M::load(kg + (int64_t)j * DP + KS * ks + PER * half);
-        PRow<T, DP> vr;
-        const bool vok = j < a.Tk;
-        vr.load((const T*)a.v + b * a.vs.sb + (int64_t)(vok ? j : 0) * a.vs.st + h * a.vs.sh, vok, a.D, half);
-        float isv[16];
-        {
-          const float iv = vr.inv_norm(a.eps);
-          wave_lds_sync();
-          if (half == 0) sv[w][m] = iv;
-          wave_lds_sync();
-          read_row_scales(sv[w], half, isv);
-        }
-
-        f32x16 s;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(kf[ks], qf[ks], s);
-        guard_frags(kf);
-
-        // P^T[j][i] = alpha_ij m_ij / |v_j|; register r -> key
-        // k0 + 32kh + rowof(r, half), lane -> query i
-        const int rel0 = i - (k0 + 32 * kh + 8 * half);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-          const float av = trim(s[r] * iq, hp.r);
-          const bool pos = av > 0.0f;
-          float p = 0.0f;
-          if (__ballot(pos) != 0ull) {
-            if (pos && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
-          }
-          s[r] = p;
-        }
-        // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
-        frag pb[NC], ta[NDH * NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) pb[c] = M::pack(s, c * PER);
-        {
-          f32x16 tr[NDH];
-          transpose_rows<T, DP>(vr.f, id, tr);
-#pragma unroll
-          for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-        }
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int dblk = 0; dblk < NDH; ++dblk) o[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], o[dblk]);
-        guard_frags(vr.f);
-        guard_frags(ta);
-        guard_frags(pb);
+    for (int r = 0; r < 16; ++r) {
+      const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+      const float av = trim(s[r] * iq, hp.r);
+      const bool pos = av > 0.0f;
+      float p = 0.0f;
+      if (__ballot(pos) != 0ull) {
+        if (pos && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
       }
+      s[r] = p;
     }
-    guard_frags(qf);
-    guard_frags(id);
-  }
+    // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
+    frag pb[NC], ta[NDH * NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) pb[c] = M::pack(s, c * PER);
+    {
+      f32x16 tr[NDH];
+      transpose_rows<T, DP>(va, id, tr);
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk) o[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], o[dblk]);
+    guard_frags(va);
+    guard_frags(ta);
+    guard_frags(pb);
 
+    cur = nxt;
+    nxt = walk.next();
+  }
+  guard_frags(qf);
+  guard_frags(id);
+
+  // the kh = 1 wave's H^T reaches the kh = 0 wave through the (now idle)
+  // stage buffers
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&stage[0][0]);  // [qh][NDH][16][64]
   if (kh == 1) {
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[qh][dblk][r][lane] = o[dblk][r];
+      for (int r = 0; r < 16; ++r) red[((qh * NDH + dblk) * 16 + r) * kWave + lane] = o[dblk][r];
   }
   __syncthreads();
   if (kh == 1) return;
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[dblk][r] += red[qh][dblk][r][lane];
+    for (int r = 0; r < 16; ++r) o[dblk][r] += red[((qh * NDH + dblk) * 16 + r) * kWave + lane];
 
   // TanhNorm per query row (lane -> query, registers -> d), y in (B,T,H,D)
   float ss = 0.0f;
@@ -474,9 +513,8 @@ void fwd_live_kernel(FwdKArgs a) {
   const float n = sqrtf(ss);
   const float nc = fmaxf(n, a.eps);
   const float f = tanhf(nc) / nc;
-  if (i < a.Tq) {
+  if (valid) {
     if (half == 0) a.hnorm[(int64_t)bh * a.Tq + i] = n;
-    T* yrow = (T*)a.y + (((int64_t)b * a.Tq + i) * a.H + h) * a.D;
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll

@@ -26,7 +26,9 @@ struct Strides3 { int64_t sb, st, sh; };
 // padded and masked keys) that the forward stages through LDS.
 size_t fwd_ws_bytes(const Geometry& g);
 
-// Backward workspace: part [2][b*h][nkt] fp32 per-wave partial sums of dr, dw.
+// Backward workspace: per-key-tile partial sums of dr, dw ([2][b*h][nkt]
+// fp32), then dh ([b*h][Tq_pad][DP] in the input type) and 1/|q|
+// ([b*h][Tq_pad] fp32) that dq_kernel hands to dkdv_kernel.
 size_t bwd_ws_bytes(const Geometry& g);
 
 struct FwdCall {
@@ -51,7 +53,7 @@ struct BwdCall {
   float eps;
   const void* y; const float* hnorm; const void* dy;
   const uint32_t* bits;
-  float* part;
+  void* workspace;
   void* dq; void* dk; void* dv; float* dr; float* dw;
   hipStream_t stream;
 };
