@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
   const int half = lane >> 5, l32 = lane & 31;
   int qt, bh;
-  xcd_order(qt, bh);
+  xcd_interleave(qt, bh);
   const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
@@ -270,13 +270,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     {
       float s2k = 0.0f, s2v = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          const float xk = M::get(ka[ks], e), xv = M::get(va[ks], e);
-          s2k += xk * xk;
-          s2v += xv * xv;
-        }
+      for (int ks = 0; ks < NKS; ++ks) {
+        s2k = frag_dot(ka[ks], ka[ks], s2k);
+        s2v = frag_dot(va[ks], va[ks], s2v);
+      }
       s2k += __shfl_xor(s2k, 32);
       s2v += __shfl_xor(s2v, 32);
       const float ik = (jok && mk_cur == 0) ? 1.0f / fmaxf(sqrtf(s2k), a.eps) : 0.0f;
@@ -288,10 +285,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       read_row_scales(sv[w], half, isv);
     }
 
-    // S^T = K Q^T, dP^T = V dH^T; K^T by identity, packed at once as the A
-    // operand of the dQ product
+    // S^T = K Q^T, dP^T = V dH^T
     f32x16 s, dp;
-    frag kta[NDH * NC];
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
 #pragma unroll
@@ -299,40 +294,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       s = M::mma_ng(ka[ks], qb[ks], s);
       dp = M::mma_ng(va[ks], hb[ks], dp);
     }
-    {
-      f32x16 tr[NDH];
-      transpose_rows<T, DP>(ka, id, tr);
+    // pre-square values; register r -> key k0 + 32kh + rowof(r, half), lane -> query i
+    bool anyp = false;
 #pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk)
+    for (int r = 0; r < 16; ++r) {
+      s[r] = trim(s[r] * isk[r] * iql, hp.r);
+      anyp |= s[r] > 0.0f;
+    }
+    // only a quadrant with a pair past the threshold contributes to dq
+    if (__ballot(anyp) != 0ull) {
+      frag kta[NDH * NC];  // K^T by identity, packed as the A operand of the dQ product
+      {
+        f32x16 tr[NDH];
+        transpose_rows<T, DP>(ka, id, tr);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) kta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+        for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) kta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+      }
+      const int rel0 = i - (k0 + 32 * kh + 8 * half);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+        const float av = s[r];
+        float ds = 0.0f;
+        if (av > 0.0f && valid && in_window(dd, hp.wc, causal))
+          ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+        dp[r] = ds * isk[r];
+      }
+      // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
+      frag db[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int dblk = 0; dblk < NDH; ++dblk) adq[dblk] = M::mma_ng(kta[dblk * NC + c], db[c], adq[dblk]);
+      guard_frags(db);
+      guard_frags(kta);
     }
     guard_frags(ka);
     guard_frags(va);
-
-    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i
-    const int rel0 = i - (k0 + 32 * kh + 8 * half);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-      const float av = trim(s[r] * isk[r] * iql, hp.r);
-      const bool pos = av > 0.0f;
-      float ds = 0.0f;
-      if (__ballot(pos) != 0ull) {
-        if (pos && valid && in_window(dd, hp.wc, causal)) ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
-      }
-      dp[r] = ds * isk[r];
-    }
-    // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
-    frag db[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk) adq[dblk] = M::mma_ng(kta[dblk * NC + c], db[c], adq[dblk]);
-    guard_frags(db);
-    guard_frags(kta);
 
     cur = nxt;
     mk_cur = mk_nxt;
@@ -393,7 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
   const int half = lane >> 5, l32 = lane & 31;
   int kt, bh;
-  xcd_order(kt, bh);
+  xcd_interleave(kt, bh);
   const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
@@ -512,17 +514,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       guard_frags(vf);
     }
 
-    // register r -> query q0 + 32qh + rowof(r, half), lane -> key j
-    const int rel0 = (q0 + 32 * qh + 8 * half) - j;
+    // similarities s (in place); register r -> query q0 + 32qh + rowof(r, half),
+    // lane -> key j.  Only a quadrant with a pair past the threshold
+    // contributes to dk, dv, dr, dw.
+    bool anyp = false;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-      const float sv = s[r] * isq[r] * ikl;
-      const float av = trim(sv, hp.r);
-      const bool pos = av > 0.0f;
-      float p = 0.0f, ds = 0.0f;
-      if (__ballot(pos) != 0ull) {
-        if (pos && in_window(dd, hp.wc, causal)) {
+      s[r] = s[r] * isq[r] * ikl;
+      anyp |= trim(s[r], hp.r) > 0.0f;
+    }
+    if (__ballot(anyp) != 0ull) {
+      const int rel0 = (q0 + 32 * qh + 8 * half) - j;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = rel0 + 16 * (r >> 3) + (r & 7);
+        const float sv = s[r];
+        const float av = trim(sv, hp.r);
+        float p = 0.0f, ds = 0.0f;
+        if (av > 0.0f && in_window(dd, hp.wc, causal)) {
           const float mk = softmask(dd, hp.iw);
           const float g = dp[r] * ivl;
           p = av * av * mk;
@@ -530,19 +539,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
           dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
           dw_acc += av * av * g * softmask_dw(dd, hp.iw);
         }
+        s[r] = p;
+        dp[r] = ds * isq[r];
       }
-      s[r] = p;
-      dp[r] = ds * isq[r];
-    }
-    // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
-    // with dH^T, Q^T from identity products (packed A operands)
-    frag pb[NC], db[NC];
+      // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
+      // with dH^T, Q^T from identity products (packed A operands)
+      frag pb[NC], db[NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      pb[c] = M::pack(s, c * PER);
-      db[c] = M::pack(dp, c * PER);
-    }
-    {
+      for (int c = 0; c < NC; ++c) {
+        pb[c] = M::pack(s, c * PER);
+        db[c] = M::pack(dp, c * PER);
+      }
       frag ta[NDH * NC];
       f32x16 tr[NDH];
       transpose_rows<T, DP>(ha, id, tr);
@@ -565,11 +572,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
 #pragma unroll
         for (int dblk = 0; dblk < NDH; ++dblk) acc_k[dblk] = M::mma_ng(ta[dblk * NC + c], db[c], acc_k[dblk]);
       guard_frags(ta);
+      guard_frags(pb);
+      guard_frags(db);
     }
     guard_frags(qa);
     guard_frags(ha);
-    guard_frags(pb);
-    guard_frags(db);
 
     if (NBUF == 1 && nxt >= 0) {
       __syncthreads();  // every wave is done with the single buffer

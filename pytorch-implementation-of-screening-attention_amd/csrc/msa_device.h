@@ -289,6 +289,19 @@ struct Row {
   }
 };
 
+// Sum of products of two operand fragments in fp32: v_dot2c_f32_bf16 (two
+// exact bf16 products per instruction) for bf16, a plain product for fp32.
+__device__ inline float frag_dot(const bf16x8& a, const bf16x8& b, float acc) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bf16x2_t x = {a[e], a[e + 1]}, y = {b[e], b[e + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(x, y, acc, false);
+  }
+  return acc;
+}
+__device__ inline float frag_dot(float a, float b, float acc) { return acc + a * b; }
+
 // An operand row kept in its storage type: the lane's NKS fragments (slots
 // d = KS*ks + PER*half + e), converted to fp32 only where arithmetic needs it.
 template <typename T, int DP>
@@ -313,9 +326,7 @@ struct PRow {
   __device__ inline float dot(const PRow& o) const {
     float s = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-      for (int e = 0; e < PER; ++e) s += M::get(f[ks], e) * M::get(o.f[ks], e);
+    for (int ks = 0; ks < NKS; ++ks) s = frag_dot(f[ks], o.f[ks], s);
     return s + __shfl_xor(s, 32);
   }
   __device__ inline float inv_norm(float eps) const { return 1.0f / fmaxf(sqrtf(dot(*this)), eps); }
@@ -429,6 +440,26 @@ struct BitWalk {
     return idx;
   }
 };
+
+// Balanced XCD mapping for kernels with one block per (tile, head).  Blocks
+// are dispatched round-robin over the 8 XCDs in linear order (x fastest).
+// With nx % 8 == 0, XCD x receives tiles x, x+8, x+16, ... of every head,
+// head after head: each XCD gets an equal share of every head's rows (whose
+// cost depends on the head's window and threshold), and the blocks it runs
+// at one time cover a few heads, so neighbouring tiles share its L2.  Within
+// a head the highest tiles come first.
+__device__ inline void xcd_interleave(int& bx, int& by) {
+  const int nx = gridDim.x;
+  if ((nx & 7) == 0) {
+    const int p = blockIdx.x + nx * blockIdx.y;
+    const int x = p & 7, s = p >> 3, per = nx >> 3;
+    by = s / per;
+    bx = nx - 1 - ((s - by * per) * 8 + x);
+  } else {
+    by = blockIdx.y;
+    bx = nx - 1 - blockIdx.x;
+  }
+}
 
 // XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs
 // in linear order (x fastest); when the grid divides evenly, remap so each

@@ -90,11 +90,11 @@ __device__ inline void load_q_tile(const FwdKArgs& a, int b, int h, int q0, bool
   for (int qh = 0; qh < 2; ++qh) {
     const int i = q0 + 32 * qh + l32;
     const bool ok = wave_ok && i < a.Tq;
-    Row<T, DP> row;
+    PRow<T, DP> row;
     row.load((const T*)a.q + b * a.qs.sb + (int64_t)(ok ? i : 0) * a.qs.st + h * a.qs.sh, ok, a.D, half);
     iq[qh] = row.inv_norm(a.eps);
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = row.frag(ks, 1.0f);
+    for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = row.f[ks];
   }
 }
 
@@ -127,6 +127,35 @@ struct ScreenTile {
 };
 constexpr int kScreenSegBlocks = 8;  // max blocks per query-tile group
 
+// Block order of the screen.  A head's cost grows with its window, and its
+// key tiles are re-read by every query group, so a head stays on one XCD (one
+// L2) and the heads are dealt to the 8 XCDs by window size: ranks (widest
+// first) 0..7 go to XCDs 0..7, ranks 8..15 to XCDs 7..0, and so on, which
+// evens out the XCDs' total work.  Each XCD runs its heads widest first and,
+// within a head, the longest (last) query groups first.  Blocks are
+// dispatched round-robin over the XCDs in linear order, so linear block p
+// runs on XCD p % 8.  Other shapes fall back to xcd_order.
+__device__ inline void screen_order(const FwdKArgs& a, int& bx, int& bh) {
+  const int nx = gridDim.x, BH = gridDim.y;
+  if ((BH & 7) != 0 || BH > 64) {
+    xcd_order(bx, bh);
+    return;
+  }
+  const int p = blockIdx.x + nx * blockIdx.y;
+  const int x = p & 7, s = p >> 3;
+  const int jh = s / nx;                                 // this XCD's jh-th head
+  const int k = 8 * jh + ((jh & 1) ? 7 - x : x);         // its rank, widest first
+  const int lane = threadIdx.x & 63;
+  const float wl = lane < BH ? a.w[lane % a.H] : 0.0f;
+  int rank = 0;
+  for (int o = 0; o < BH; ++o) {
+    const float wo = a.w[o % a.H];
+    rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
+  }
+  bh = __builtin_ctzll(__ballot(lane < BH && rank == k));
+  bx = nx - 1 - (s - jh * nx);
+}
+
 // ---------------------------------------------------------------------------
 // Screen: 256-thread block = 4 waves, wave -> one 64-query tile of one head.
 // The key-tile range of the 4 tiles' windows is cut into segments of SEG
@@ -152,7 +181,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
   const int half = lane >> 5, l32 = lane & 31;
   int bx, bh;
-  xcd_order(bx, bh);
+  screen_order(a, bx, bh);
   const int grp = bx / a.nsegl, seg0 = bx % a.nsegl;
   const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
@@ -340,7 +369,7 @@ void fwd_live_kernel(FwdKArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
   const int half = lane >> 5, l32 = lane & 31;
   int qt, bh;
-  xcd_order(qt, bh);
+  xcd_interleave(qt, bh);
   const int b = bh / a.H, h = bh % a.H;
   const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
@@ -416,24 +445,6 @@ void fwd_live_kernel(FwdKArgs a) {
       kf[ks] = S::frag(kl, 32 * kh + m, ks, half, true, DP);
       va[ks] = S::frag(vl, 32 * kh + m, ks, half, jok, a.D);
     }
-    float isv[16];
-    {
-      float s2 = 0.0f;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          const float x = M::get(va[ks], e);
-          s2 += x * x;
-        }
-      s2 += __shfl_xor(s2, 32);
-      const float iv = 1.0f / fmaxf(sqrtf(s2), a.eps);
-      wave_lds_sync();
-      if (half == 0) sv[w][m] = iv;
-      wave_lds_sync();
-      read_row_scales(sv[w], half, isv);
-    }
-
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
@@ -445,40 +456,59 @@ void fwd_live_kernel(FwdKArgs a) {
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) s = M::mma(kf[ks], qf[ks], s);
     }
-
-    // P^T[j][i] = alpha_ij m_ij / |v_j|; register r -> key
-    // k0 + 32kh + rowof(r, half), lane -> query i
-    const int rel0 = i - (k0 + 32 * kh + 8 * half);
+    // pre-square values (in place); register r -> key k0 + 32kh + rowof(r, half),
+    // lane -> query i.  Only a quadrant with a pair past the threshold
+    // contributes to h.
+    bool anyp = false;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-      const float av = trim(s[r] * iq, hp.r);
-      const bool pos = av > 0.0f;
-      float p = 0.0f;
-      if (__ballot(pos) != 0ull) {
-        if (pos && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
+      s[r] = trim(s[r] * iq, hp.r);
+      anyp |= s[r] > 0.0f;
+    }
+    if (__ballot(anyp) != 0ull) {
+      // 1/|v_j| in register order
+      float isv[16];
+      {
+        float s2 = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) s2 = frag_dot(va[ks], va[ks], s2);
+        s2 += __shfl_xor(s2, 32);
+        const float iv = 1.0f / fmaxf(sqrtf(s2), a.eps);
+        wave_lds_sync();
+        if (half == 0) sv[w][m] = iv;
+        wave_lds_sync();
+        read_row_scales(sv[w], half, isv);
       }
-      s[r] = p;
+      // P^T[j][i] = alpha_ij m_ij / |v_j|
+      const int rel0 = i - (k0 + 32 * kh + 8 * half);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+        const float av = s[r];
+        float p = 0.0f;
+        if (av > 0.0f && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
+        s[r] = p;
+      }
+      // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
+      frag pb[NC], ta[NDH * NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) pb[c] = M::pack(s, c * PER);
+      {
+        f32x16 tr[NDH];
+        transpose_rows<T, DP>(va, id, tr);
+#pragma unroll
+        for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int dblk = 0; dblk < NDH; ++dblk) o[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], o[dblk]);
+      guard_frags(ta);
+      guard_frags(pb);
     }
-    // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
-    frag pb[NC], ta[NDH * NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) pb[c] = M::pack(s, c * PER);
-    {
-      f32x16 tr[NDH];
-      transpose_rows<T, DP>(va, id, tr);
-#pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-    }
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk) o[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], o[dblk]);
     guard_frags(va);
-    guard_frags(ta);
-    guard_frags(pb);
 
     cur = nxt;
     nxt = walk.next();
