@@ -104,47 +104,34 @@ __device__ inline void key_rows(const BwdKArgs& a, int b, int h, int j, int half
   if (!ok || masked) ik = 0.0f;
 }
 
-// Writes dx = normalise-backward(dx^, x) for one row held in C-layout
-// registers acc[dh] (rows d = 32*dh + 8*(r/4) + 4*half + r%4) of a lane.
-template <typename T, int NDH>
-__device__ inline void write_norm_bwd(const f32x16 (&acc)[NDH], const T* xrow, bool valid, int D, float eps,
-                                      int half, T* out) {
-  f32x4 xv[NDH][4];
+// Writes dx = normalise-backward(dx^, x) (attention.py:156-158 under
+// autograd) for one row: dx^ in C-layout registers acc[dblk] whose rows are
+// tcol-ordered columns, x as the lane's raw operand fragments of the same row
+// (the operands the kernel already holds, so nothing is re-read).
+//   |x| > eps:  dx = (dx^ - x^ (x^ . dx^)) / |x|;   otherwise dx = dx^ / eps.
+template <typename T, int DP>
+__device__ inline void write_norm_bwd(const f32x16 (&acc)[DP / 32], const typename Mma<T>::frag (&x)[DP / Mma<T>::KS],
+                                      bool valid, int D, float eps, int half, T* out) {
+  using M = Mma<T>;
+  constexpr int NDH = DP / 32, NKS = DP / M::KS;
   float ss = 0.0f;
 #pragma unroll
-  for (int dh = 0; dh < NDH; ++dh)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * dh + 8 * g + 4 * half;
-      xv[dh][g] = (valid && d < D) ? load4(xrow + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ss += xv[dh][g][e] * xv[dh][g][e];
-    }
+  for (int ks = 0; ks < NKS; ++ks) ss = frag_dot(x[ks], x[ks], ss);
   ss += __shfl_xor(ss, 32);
   const float nx = sqrtf(ss);
   const float ix = 1.0f / fmaxf(nx, eps);
   float dot = 0.0f;
 #pragma unroll
-  for (int dh = 0; dh < NDH; ++dh)
+  for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dot += xv[dh][g][e] * ix * acc[dh][4 * g + e];
+    for (int r = 0; r < 16; ++r) dot += M::get(x[creg_ks<T>(dblk, r)], creg_e<T>(r)) * ix * acc[dblk][r];
   dot += __shfl_xor(dot, 32);
   const float proj = nx > eps ? dot : 0.0f;
   if (!valid) return;
-#pragma unroll
-  for (int dh = 0; dh < NDH; ++dh)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * dh + 8 * g + 4 * half;
-      if (d < D) {
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (acc[dh][4 * g + e] - xv[dh][g][e] * ix * proj) * ix;
-        store4(out + d, o[0], o[1], o[2], o[3]);
-      }
-    }
+  store_creg_row<T, NDH>(out, D, half, [&](int dblk, int r) {
+    const float xn = M::get(x[creg_ks<T>(dblk, r)], creg_e<T>(r)) * ix;
+    return (acc[dblk][r] - xn * proj) * ix;
+  });
 }
 
 // Waves per SIMD the backward kernels are register-budgeted for: two (256
@@ -169,8 +156,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   using frag = typename M::frag;
   using S = StageTile<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  __shared__ __attribute__((aligned(16))) char stage[2][2 * S::TILEB];  // [buffer][K tile | V tile]
-  __shared__ __attribute__((aligned(16))) float sk[4][32];              // per wave: 1/|k| (0 if masked)
+  // DMA ring of staged key tiles: NBUF buffers, NBUF-1 tiles ahead
+  constexpr int NBUF = 3 * 2 * S::TILEB <= 100 * 1024 ? 3 : 2;
+  constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile
+  __shared__ __attribute__((aligned(16))) char stage[NBUF][2 * S::TILEB];  // [buffer][K tile | V tile]
+  __shared__ __attribute__((aligned(16))) float sk[4][32];                 // per wave: 1/|k| (0 if masked)
   __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v|
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
@@ -217,8 +207,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     const int j = kt * kTile + 32 * kh + m;
     msk = (a.kpm != nullptr && j < a.Tk) ? a.kpm[(int64_t)b * a.Tk + j] : (uint8_t)0;
   };
-  uint8_t mk_cur, mk_nxt = 0;
-  stage_tile(cur, 0, mk_cur);
+  // tl[n]: the n-th next live key tile (-1 past the end); mk[n] its key-padding byte
+  int tl[3] = {cur, -1, -1};
+  uint8_t mk[3] = {0, 0, 0};
+  stage_tile(tl[0], 0, mk[0]);
+  for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
+  if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1, mk[1]);
 
   // own queries as raw B operands (lane -> query) and dh, overlapping the DMA
   frag qb[NKS], hb[NKS];
@@ -247,13 +241,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
 #pragma unroll
     for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
 
-  int nxt = walk.next();
-  for (int it = 0; cur >= 0; ++it) {
-    wait_vmcnt<0>();
-    __syncthreads();  // tile `cur` is in LDS; the other buffer is free
-    if (nxt >= 0) stage_tile(nxt, (it + 1) & 1, mk_nxt);
-    const char* kl = stage[it & 1];
+  for (int it = 0; tl[0] >= 0; ++it) {
+    // tile tl[0] is in LDS once this wave's older DMA is done and every wave
+    // passed the barrier; the buffer refilled next was read last iteration
+    if (NBUF == 3 && tl[1] >= 0) wait_vmcnt<PT>();
+    else wait_vmcnt<0>();
+    block_sync_lds();
+    if (tl[NBUF - 1] >= 0) stage_tile(tl[NBUF - 1], (it + NBUF - 1) % NBUF, mk[NBUF - 1]);
+    const char* kl = stage[it % NBUF];
     const char* vl = kl + S::TILEB;
+    const int cur = tl[0];
+    const uint8_t mk_cur = mk[0];
     const int k0 = cur * kTile;
 
     // key rows j = k0 + 32*kh + perm_row(l32) as A operands, with 1/|k|
@@ -336,9 +334,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     guard_frags(ka);
     guard_frags(va);
 
-    cur = nxt;
-    mk_cur = mk_nxt;
-    nxt = walk.next();
+#pragma unroll
+    for (int n = 0; n < NBUF - 1; ++n) { tl[n] = tl[n + 1]; mk[n] = mk[n + 1]; }
+    tl[NBUF - 1] = walk.next();
   }
   guard_frags(qb);
   guard_frags(hb);
@@ -360,8 +358,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
       for (int r = 0; r < 16; ++r) adq[dblk][r] += red[((qh * NDH + dblk) * 16 + r) * kWave + lane];
-    write_norm_bwd<T, NDH>(adq, (const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, valid, a.D,
-                           a.eps, half, dqrow);
+    write_norm_bwd<T, DP>(adq, qb, valid, a.D, a.eps, half, dqrow);
   }
 }
 
@@ -386,7 +383,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   constexpr int SB = 2 * S::TILEB + 1024;  // per buffer: Q tile | dh tile | 1/|q| (64 floats, 1 KB slot)
   constexpr int KVB = 2 * NKS * kWave * (int)sizeof(frag);  // per key half: own K, V fragments
-  constexpr int NBUF = 2 * SB + 2 * KVB <= 150 * 1024 ? 2 : 1;  // double-buffer where LDS allows
+  // DMA ring of staged query tiles: NBUF buffers, NBUF-1 tiles ahead where LDS allows
+  constexpr int NBUF = 3 * SB + 2 * KVB <= 70 * 1024 ? 3 : (2 * SB + 2 * KVB <= 150 * 1024 ? 2 : 1);
+  constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile (wave 0 issues one more)
   static_assert(4 * NDH * 16 * kWave * 4 <= NBUF * SB, "exchange must fit the stage buffers");
   __shared__ __attribute__((aligned(16))) char stage[NBUF][SB];
   __shared__ __attribute__((aligned(16))) char kvs[2][KVB];
@@ -445,7 +444,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
           (const void __attribute__((address_space(1)))*)(iq0 + (int64_t)qt * kTile + 4 * (lane < 16 ? lane : 15)),
           (void __attribute__((address_space(3)))*)(stage[buf] + 2 * S::TILEB), 16, 0, 0);
   };
-  stage_tile(cur, 0);
+  // tl[n]: the n-th next live query tile (-1 past the end)
+  int tl[3] = {cur, -1, -1};
+  stage_tile(tl[0], 0);
+  for (int n = 1; n < (NBUF > 1 ? NBUF : 2); ++n) tl[n] = walk.next();
 
   // own keys as raw B operands (lane -> key), kept in LDS (one copy per key
   // half, written by its qh = 0 wave before the loop's first barrier), with
@@ -473,15 +475,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   float dr_acc = 0.0f, dw_acc = 0.0f;
   const int m = perm_row(l32);
 
-  int nxt = walk.next();
-  for (int it = 0; cur >= 0; ++it) {
-    wait_vmcnt<0>();
-    __syncthreads();  // tile `cur` is in LDS; with two buffers the other one is free
-    if (NBUF == 2 && nxt >= 0) stage_tile(nxt, (it + 1) & 1);
-    const char* ql = stage[NBUF == 2 ? (it & 1) : 0];
+  if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
+  for (int it = 0; tl[0] >= 0; ++it) {
+    // tile tl[0] is in LDS once this wave's older DMA is done and every wave
+    // passed the barrier; the buffer refilled next was read last iteration
+    if (NBUF == 3 && tl[1] >= 0) wait_vmcnt<PT>();
+    else wait_vmcnt<0>();
+    block_sync_lds();
+    if (NBUF > 1 && tl[NBUF - 1] >= 0) stage_tile(tl[NBUF - 1], (it + NBUF - 1) % NBUF);
+    const char* ql = stage[it % NBUF];
     const char* hl = ql + S::TILEB;
     const float* iql = reinterpret_cast<const float*>(ql + 2 * S::TILEB);
-    const int q0 = cur * kTile;
+    const int q0 = tl[0] * kTile;
 
     // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
     const bool iok = q0 + 32 * qh + m < a.Tq;
@@ -578,12 +583,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     guard_frags(qa);
     guard_frags(ha);
 
-    if (NBUF == 1 && nxt >= 0) {
-      __syncthreads();  // every wave is done with the single buffer
-      stage_tile(nxt, 0);
+    if (NBUF == 1 && tl[1] >= 0) {
+      block_sync_lds();  // every wave is done with the single buffer
+      stage_tile(tl[1], 0);
     }
-    cur = nxt;
-    nxt = walk.next();
+    tl[0] = tl[1];
+    tl[1] = tl[2];
+    tl[2] = NBUF == 3 ? walk.next() : -1;
+    if (NBUF < 3) tl[1] = walk.next();
   }
   guard_frags(id);
 
@@ -608,12 +615,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       const float other = red[(((w ^ 2) * NDH + dblk) * 16 + r) * kWave + lane];
       fin[dblk][r] = qh == 0 ? acc_k[dblk][r] + other : other + acc_v[dblk][r];
     }
-  if (qh == 0)
-    write_norm_bwd<T, NDH>(fin, (const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, jvalid, a.D,
-                           a.eps, half, (T*)a.dk + orow);
-  else
-    write_norm_bwd<T, NDH>(fin, (const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, jvalid, a.D,
-                           a.eps, half, (T*)a.dv + orow);
+  {
+    frag xf[NKS];  // own raw k (qh = 0) or v (qh = 1) rows, from LDS
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) xf[ks] = kvl[(qh * NKS + ks) * kWave + lane];
+    write_norm_bwd<T, DP>(fin, xf, jvalid, a.D, a.eps, half, (T*)(qh == 0 ? a.dk : a.dv) + orow);
+  }
   if (tid == 0) {
     const int64_t nbh = (int64_t)a.B * a.H;
     a.part[(int64_t)bh * a.nkt + kt] = (rw[0][0] + rw[0][1]) + (rw[0][2] + rw[0][3]);

@@ -133,21 +133,45 @@ __device__ inline int rowof(int r, int half) { return 16 * (r >> 3) + 8 * half +
 
 // Transpose by MFMA.  For 32 rows X held as A fragments x[ks] (lane l%32 ->
 // row perm_row(l%32), slots -> columns d = KS*ks + PER*(l/32) + e), the product
-// X I with the identity gives, per 32-column block dblk, a C block with
-// lane -> column d = 32*dblk + l%32 and register r -> X row rowof(r, l/32).
-// Packed PER registers at a time, that is the A operand of a second product
-// that contracts over X's rows with a C block over the same rows (register
-// index = contraction index on both sides).  Products with 1 and sums with 0
-// are exact, so the values come through unchanged.
-// Slice c of the identity (k-step c of a 32-column block; it does not depend
-// on the block): slot e of lane l is 1 iff KS*c + PER*(l/32) + e == l%32.
+// X P with a permutation matrix gives, per 32-column block dblk, a C block with
+// lane -> column d = 32*dblk + tcol(l%32) and register r -> X row
+// rowof(r, l/32).  Packed PER registers at a time, that is the A operand of a
+// second product that contracts over X's rows with a C block over the same
+// rows (register index = contraction index on both sides).  Products with 1
+// and sums with 0 are exact, so the values come through unchanged.
+// The column order tcol makes the second product's C block (rows = X's
+// columns) put, in each lane, the columns that lane holds of an operand row
+// fragment: register r of block dblk <-> fragment (ks, e) = creg_frag(dblk, r)
+// (see below), so a row-wise epilogue can combine the accumulator with the
+// operand fragments it already has, and store 16 contiguous bytes per group.
+template <typename T>
+__device__ inline int tcol(int m) {
+  if constexpr (sizeof(T) == 2) return perm_row(m);                 // 16*(m/16) + 8*((m>>2)&1) + ...
+  else return 8 * (m >> 3) + 2 * (m & 3) + ((m >> 2) & 1);
+}
+// Fragment slot (ks, e) that holds, in the same lane, the column that register
+// r of C block dblk covers when the block's rows are tcol-ordered columns.
+template <typename T>
+__device__ constexpr int creg_ks(int dblk, int r) {
+  if constexpr (sizeof(T) == 2) return 2 * dblk + (r >> 3);   // column 32*dblk + 16*(r/8) + 8*half + r%8
+  else return 16 * dblk + 4 * (r >> 2) + (r & 3);             // column 32*dblk + 8*(r/4) + 2*(r%4) + half
+}
+template <typename T>
+__device__ constexpr int creg_e(int r) {
+  if constexpr (sizeof(T) == 2) return r & 7;
+  else return 0;
+}
+// Slice c of the permutation (k-step c of a 32-column block; it does not
+// depend on the block): slot e of lane l is 1 iff KS*c + PER*(l/32) + e ==
+// tcol(l%32).
 template <typename T>
 __device__ inline typename Mma<T>::frag ident_frag(int c, int lane) {
   using M = Mma<T>;
   const int l32 = lane & 31, half = lane >> 5;
+  const int want = tcol<T>(l32);
   f32x16 t;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) t[e] = (e < M::PER && M::KS * c + M::PER * half + e == l32) ? 1.0f : 0.0f;
+  for (int e = 0; e < 16; ++e) t[e] = (e < M::PER && M::KS * c + M::PER * half + e == want) ? 1.0f : 0.0f;
   return M::pack(t, 0);
 }
 // out[dblk] = (X I)[:, 32*dblk .. 32*dblk+31] with unguarded MFMAs: the
@@ -233,6 +257,47 @@ __device__ inline void store4(float* p, float a, float b, float c, float d) {
 __device__ inline void store4(bf16* p, float a, float b, float c, float d) {
   *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a, (bf16)b, (bf16)c, (bf16)d};
 }
+// Stores 8 consecutive values (16 bytes for bf16).
+__device__ inline void store8(bf16* p, const float (&v)[8]) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
+  *reinterpret_cast<bf16x8*>(p) = o;
+}
+__device__ inline void store8(float* p, const float (&v)[8]) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+// Writes one row held in C-layout registers whose rows are tcol-ordered
+// columns (a product with a transpose_rows operand): value(dblk, r) -> column
+// 32*dblk + (column of register r).  fn(dblk, r) gives the value.
+template <typename T, int NDH, typename Fn>
+__device__ inline void store_creg_row(T* row, int D, int half, Fn fn) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int d0 = 32 * dblk + 16 * g + 8 * half;
+        if (d0 < D) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = fn(dblk, 8 * g + e);
+          store8(row + d0, v);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * dblk + 8 * (r >> 2) + 2 * (r & 3) + half;
+        if (d < D) row[d] = fn(dblk, r);
+      }
+  }
+}
+
 // Loads 4 consecutive values as fp32.
 __device__ inline f32x4 load4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ inline f32x4 load4(const bf16* p) {
@@ -359,6 +424,16 @@ __device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]
 // stores and global->LDS DMA) are outstanding.
 template <int N>
 __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
+
+// Block barrier for LDS hand-over that leaves vector memory traffic (e.g. DMA
+// prefetches into other buffers) in flight: this wave's LDS operations
+// complete, then s_barrier.  The asm statements keep the compiler from moving
+// memory operations across it.
+__device__ inline void block_sync_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // Waits for this wave's LDS traffic and keeps the compiler from moving
 // memory operations across the point (LDS ops of one wave run in order).

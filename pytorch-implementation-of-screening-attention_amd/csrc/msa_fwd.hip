@@ -363,7 +363,10 @@ void fwd_live_kernel(FwdKArgs a) {
   using frag = typename M::frag;
   using S = StageTile<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  __shared__ __attribute__((aligned(16))) char stage[2][2 * S::TILEB];  // [buffer][K^ tile | V tile]
+  // DMA ring of staged key tiles: NBUF buffers, NBUF-1 tiles ahead
+  constexpr int NBUF = 3 * 2 * S::TILEB <= 100 * 1024 ? 3 : 2;
+  constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile
+  __shared__ __attribute__((aligned(16))) char stage[NBUF][2 * S::TILEB];  // [buffer][K^ tile | V tile]
   __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v_j| of its key rows
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
@@ -404,7 +407,11 @@ void fwd_live_kernel(FwdKArgs a) {
     S::issue(kg, DP, (int64_t)kt * kTile, a.Tk_pad, DP, stage[buf], tid, w);
     S::issue(vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
   };
-  stage_tile(cur, 0);
+  // tl[n]: the n-th next live key tile (-1 past the end)
+  int tl[3] = {cur, -1, -1};
+  stage_tile(tl[0], 0);
+  for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
+  if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
 
   // own queries as raw B operands (lane -> query) and 1/|q_i|, overlapping the DMA
   frag qf[NKS];
@@ -426,14 +433,16 @@ void fwd_live_kernel(FwdKArgs a) {
     for (int r = 0; r < 16; ++r) o[dblk][r] = 0.0f;
   const int m = perm_row(l32);
 
-  int nxt = walk.next();
-  for (int it = 0; cur >= 0; ++it) {
-    wait_vmcnt<0>();
-    __syncthreads();  // tile `cur` is in LDS; the other buffer is free
-    if (nxt >= 0) stage_tile(nxt, (it + 1) & 1);
-    const char* kl = stage[it & 1];
+  for (int it = 0; tl[0] >= 0; ++it) {
+    // tile tl[0] is in LDS once this wave's older DMA is done and every wave
+    // passed the barrier; the buffer refilled next was read last iteration
+    if (NBUF == 3 && tl[1] >= 0) wait_vmcnt<PT>();
+    else wait_vmcnt<0>();
+    block_sync_lds();
+    if (tl[NBUF - 1] >= 0) stage_tile(tl[NBUF - 1], (it + NBUF - 1) % NBUF);
+    const char* kl = stage[it % NBUF];
     const char* vl = kl + S::TILEB;
-    const int k0 = cur * kTile;
+    const int k0 = tl[0] * kTile;
 
     // key rows j = k0 + 32*kh + perm_row(l32): K^ (zero past Tk) and raw V
     // with 1/|v|
@@ -510,8 +519,9 @@ void fwd_live_kernel(FwdKArgs a) {
     }
     guard_frags(va);
 
-    cur = nxt;
-    nxt = walk.next();
+#pragma unroll
+    for (int n = 0; n < NBUF - 1; ++n) tl[n] = tl[n + 1];
+    tl[NBUF - 1] = walk.next();
   }
   guard_frags(qf);
   guard_frags(id);
@@ -545,14 +555,7 @@ void fwd_live_kernel(FwdKArgs a) {
   const float f = tanhf(nc) / nc;
   if (valid) {
     if (half == 0) a.hnorm[(int64_t)bh * a.Tq + i] = n;
-#pragma unroll
-    for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = 32 * dblk + 8 * g + 4 * half;
-        if (d < a.D)
-          store4(yrow + d, f * o[dblk][4 * g], f * o[dblk][4 * g + 1], f * o[dblk][4 * g + 2], f * o[dblk][4 * g + 3]);
-      }
+    store_creg_row<T, NDH>(yrow, a.D, half, [&](int dblk, int r) { return f * o[dblk][r]; });
   }
 }
 
