@@ -68,41 +68,53 @@ struct BwdKArgs {
   float eps;
 };
 
-// Query-side rows for row i of head (b,h): raw q with 1/|q|, and dh (rounded
-// to T, as the MFMA operand it becomes).  Rows past Tq read row 0 and are
-// zeroed.
+// Query-side rows for row i of head (b,h), in two steps so that other memory
+// traffic can be issued between them: load raw q, y, dy and |h|; then finish
+// 1/|q| and dh (rounded to T, as the MFMA operand it becomes).  Rows past Tq
+// read row 0 and are zeroed.
 template <typename T, int DP>
-__device__ inline void query_rows(const BwdKArgs& a, int b, int h, int bh, int i, int half, PRow<T, DP>& qr,
-                                  float& iq, PRow<T, DP>& dh) {
-  const bool ok = i < a.Tq;
-  const int ii = ok ? i : 0;
-  const int64_t yoff = (((int64_t)b * a.Tq + ii) * a.H + h) * a.D;
-  PRow<T, DP> yr;
-  qr.load((const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, ok, a.D, half);
-  yr.load((const T*)a.y + yoff, ok, a.D, half);
-  dh.load((const T*)a.dy + yoff, ok, a.D, half);
-  const float hn = a.hnorm[(int64_t)bh * a.Tq + ii];
-  iq = qr.inv_norm(a.eps);
-  const float ydot = yr.dot(dh);
-  float c1, c2;
-  tanhnorm_coefs(ok ? hn : 0.0f, a.eps, c1, c2);
-  dh.axpby(c1, c2 * ydot, yr);
-}
+struct QueryRows {
+  PRow<T, DP> q, y, dh;
+  float hn;
+  bool ok;
+  __device__ inline void load(const BwdKArgs& a, int b, int h, int bh, int i, int half) {
+    ok = i < a.Tq;
+    const int ii = ok ? i : 0;
+    const int64_t yoff = (((int64_t)b * a.Tq + ii) * a.H + h) * a.D;
+    q.load((const T*)a.q + b * a.qs.sb + (int64_t)ii * a.qs.st + h * a.qs.sh, ok, a.D, half);
+    y.load((const T*)a.y + yoff, ok, a.D, half);
+    dh.load((const T*)a.dy + yoff, ok, a.D, half);
+    hn = a.hnorm[(int64_t)bh * a.Tq + ii];
+  }
+  // returns 1/|q|; dh holds TanhNorm'(h)^T dy afterwards
+  __device__ inline float finish(float eps) {
+    const float iq = q.inv_norm(eps);
+    const float ydot = y.dot(dh);
+    float c1, c2;
+    tanhnorm_coefs(ok ? hn : 0.0f, eps, c1, c2);
+    dh.axpby(c1, c2 * ydot, y);
+    return iq;
+  }
+};
 
-// Key-side rows for key j of head (b,h): raw k with 1/|k| (0 for padded or
-// masked keys) and raw v with 1/|v|.
+// Key-side rows for key j of head (b,h), load then finish as for the query
+// side: raw k with 1/|k| (0 for padded or masked keys), raw v with 1/|v|.
 template <typename T, int DP>
-__device__ inline void key_rows(const BwdKArgs& a, int b, int h, int j, int half, PRow<T, DP>& kr, float& ik,
-                                PRow<T, DP>& vr, float& iv) {
-  const bool ok = j < a.Tk;
-  const int jj = ok ? j : 0;
-  kr.load((const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, ok, a.D, half);
-  vr.load((const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, ok, a.D, half);
-  const bool masked = a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + jj] != 0;
-  ik = kr.inv_norm(a.eps);
-  iv = vr.inv_norm(a.eps);
-  if (!ok || masked) ik = 0.0f;
-}
+struct KeyRows {
+  PRow<T, DP> k, v;
+  bool ok, masked;
+  __device__ inline void load(const BwdKArgs& a, int b, int h, int j, int half) {
+    ok = j < a.Tk;
+    const int jj = ok ? j : 0;
+    k.load((const T*)a.k + b * a.ks.sb + (int64_t)jj * a.ks.st + h * a.ks.sh, ok, a.D, half);
+    v.load((const T*)a.v + b * a.vs.sb + (int64_t)jj * a.vs.st + h * a.vs.sh, ok, a.D, half);
+    masked = a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + jj] != 0;
+  }
+  __device__ inline void finish(float eps, float& ik, float& iv) const {
+    ik = (ok && !masked) ? k.inv_norm(eps) : 0.0f;
+    iv = v.inv_norm(eps);
+  }
+};
 
 // Writes dx = normalise-backward(dx^, x) (attention.py:156-158 under
 // autograd) for one row: dx^ in C-layout registers acc[dblk] whose rows are
@@ -210,20 +222,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   // tl[n]: the n-th next live key tile (-1 past the end); mk[n] its key-padding byte
   int tl[3] = {cur, -1, -1};
   uint8_t mk[3] = {0, 0, 0};
-  stage_tile(tl[0], 0, mk[0]);
-  for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
-  if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1, mk[1]);
-
-  // own queries as raw B operands (lane -> query) and dh, overlapping the DMA
+  // own queries' rows first, then the first key tiles' DMA behind them
+  // (vector memory returns in order, so the rows are not held up by the DMA)
   frag qb[NKS], hb[NKS];
   float iql;
   {
-    PRow<T, DP> qr, dhr;
-    query_rows<T, DP>(a, b, h, bh, i, half, qr, iql, dhr);
+    QueryRows<T, DP> qr;
+    qr.load(a, b, h, bh, i, half);
+    stage_tile(tl[0], 0, mk[0]);
+    for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
+    if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1, mk[1]);
+    iql = qr.finish(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      qb[ks] = qr.f[ks];
-      hb[ks] = dhr.f[ks];
+      qb[ks] = qr.q.f[ks];
+      hb[ks] = qr.dh.f[ks];
     }
   }
   if (kh == 0) {  // dh and 1/|q| of this tile's rows for dkdv_kernel (zero past Tq)
@@ -446,22 +459,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   };
   // tl[n]: the n-th next live query tile (-1 past the end)
   int tl[3] = {cur, -1, -1};
-  stage_tile(tl[0], 0);
-  for (int n = 1; n < (NBUF > 1 ? NBUF : 2); ++n) tl[n] = walk.next();
-
   // own keys as raw B operands (lane -> key), kept in LDS (one copy per key
   // half, written by its qh = 0 wave before the loop's first barrier), with
-  // 1/|k| (0 if padded or masked) and 1/|v|; overlapping the first DMA
+  // 1/|k| (0 if padded or masked) and 1/|v|.  Their loads go first, the first
+  // query tile's DMA behind them (vector memory returns in order).
   frag* kvl = reinterpret_cast<frag*>(kvs[kh]);
   float ikl, ivl;
   {
-    PRow<T, DP> kr, vr;
-    key_rows<T, DP>(a, b, h, j, half, kr, ikl, vr, ivl);
+    KeyRows<T, DP> kr;
+    kr.load(a, b, h, j, half);
+    stage_tile(tl[0], 0);
+    for (int n = 1; n < (NBUF > 1 ? NBUF : 2); ++n) tl[n] = walk.next();
+    kr.finish(a.eps, ikl, ivl);
     if (qh == 0)
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        kvl[ks * kWave + lane] = kr.f[ks];
-        kvl[(NKS + ks) * kWave + lane] = vr.f[ks];
+        kvl[ks * kWave + lane] = kr.k.f[ks];
+        kvl[(NKS + ks) * kWave + lane] = kr.v.f[ks];
       }
   }
   frag id[NC];

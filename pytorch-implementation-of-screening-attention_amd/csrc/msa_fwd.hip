@@ -407,18 +407,18 @@ void fwd_live_kernel(FwdKArgs a) {
     S::issue(kg, DP, (int64_t)kt * kTile, a.Tk_pad, DP, stage[buf], tid, w);
     S::issue(vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
   };
+  // own queries as raw B operands (lane -> query) and 1/|q_i|; their loads go
+  // first, the first key tiles' DMA behind them (vector memory returns in order)
   // tl[n]: the n-th next live key tile (-1 past the end)
   int tl[3] = {cur, -1, -1};
-  stage_tile(tl[0], 0);
-  for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
-  if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
-
-  // own queries as raw B operands (lane -> query) and 1/|q_i|, overlapping the DMA
   frag qf[NKS];
   float iq;
   {
     PRow<T, DP> qr;
     qr.load((const T*)a.q + b * a.qs.sb + (int64_t)(valid ? i : 0) * a.qs.st + h * a.qs.sh, valid, a.D, half);
+    stage_tile(tl[0], 0);
+    for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
+    if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
     iq = qr.inv_norm(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
