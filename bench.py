@@ -83,6 +83,24 @@ def kernel_times(L, kid, fn, n):
     return sum(vals) / max(1, len(vals)), vals
 
 
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 byte-counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or
+    None when the summary is absent or lacks the kernel."""
+    path = os.path.join(HERE, "profiles", "fwd_bwd_cfg2_pmc_bytes.txt")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    import re
+    m = re.search(r"fetch_factor ([\d.]+) write_factor ([\d.]+)", text)
+    k = re.search(r"kernel %s\s+fetch_kib\s+([\d.]+) write_kib\s+([\d.]+)" % re.escape(kernel), text)
+    if not m or not k:
+        return None
+    ff, wf = float(m.group(1)), float(m.group(2))
+    return int((float(k.group(1)) / ff + float(k.group(2)) / wf) * 1024)
+
+
 def cpu_baseline(B, T, H, D, r, w, seed):
     """Dense reference math (torch fp32) fwd+bwd on 1 (b,h) slice of the workload."""
     import torch
@@ -241,7 +259,8 @@ def main():
                      "achieved": round(achieved, 2) if achieved else None,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 5) if achieved else None,
-                     "traffic": None,
+                     "traffic": profiled_traffic(dom),
+                     "traffic_source": "profiles/fwd_bwd_cfg2_pmc_bytes.txt",
                      "flop_per_launch": dom_flop},
         "tiles": {"causal": B * H * (T // 64) * (T // 64 + 1) // 2, "window": nW, "active": nA,
                   "window_skip": round(1 - nW / (B * H * (T // 64) * (T // 64 + 1) / 2), 4),
