@@ -3,7 +3,8 @@
 // The query at position pos = len-1 attends to keys j in (pos - w, pos]
 // (causal window, attention.py:111-118).  The window is split into chunks of
 // kChunk keys; each 256-thread block streams one chunk of raw K rows
-// (16-byte loads, D/VEC lanes per key), forms s = q^.k^ on the fly,
+// (16-byte loads, D/VEC lanes per key), forms s = q.k/(|q||k|) from exact
+// products of the raw values on the fly,
 // and reads a V row only when its alpha*m is non-zero.  Because screening has
 // no softmax normaliser (attention.py:192-193), chunk partials simply add; a
 // second kernel sums them in a fixed order and applies TanhNorm (norm.py:23-25).
@@ -13,7 +14,7 @@
 namespace msa {
 
 constexpr int kChunk = 2048;
-constexpr int kDecUnroll = 4;
+constexpr int kDecUnroll = 8;
 
 struct DecArgs {
   const void* q; int64_t q_sb, q_sh;
@@ -26,9 +27,28 @@ struct DecArgs {
   float eps;
 };
 
+// 16 bytes of a row in its storage type, and its fp32 dot products.
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> {
+  typedef bf16x8 type;
+  static constexpr int N = 8;
+  __device__ static inline float dot(const type& a, const type& b, float acc) { return frag_dot(a, b, acc); }
+  __device__ static inline float get(const type& a, int e) { return (float)a[e]; }
+};
+template <> struct Vec16<float> {
+  typedef f32x4 type;
+  static constexpr int N = 4;
+  __device__ static inline float dot(const type& a, const type& b, float acc) {
+    return acc + a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+  }
+  __device__ static inline float get(const type& a, int e) { return a[e]; }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
-  constexpr int VEC = 16 / (int)sizeof(T);  // elements per 16-byte load
+  using V = Vec16<T>;
+  using vec = typename V::type;
+  constexpr int VEC = V::N;                 // elements per 16-byte load
   constexpr int LPK = D / VEC;              // lanes per key row
   constexpr int KPW = kWave / LPK;          // keys per wave per load
   __shared__ float red[4][D];
@@ -48,66 +68,41 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
   for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
 
   if ((int64_t)blockIdx.x * kChunk < n) {
-    // query chunk and its norm (each LPK-lane group covers the whole row)
-    float qv[VEC];
-    {
-      const T* qp = (const T*)a.q + b * a.q_sb + h * a.q_sh + d0;
-      float ss = 0.0f;
+    // raw query slice and 1/|q| (each LPK-lane group covers the whole row);
+    // s = (q . k) / (|q| |k|) with exact products of the raw values
+    const vec qv = *reinterpret_cast<const vec*>((const T*)a.q + b * a.q_sb + h * a.q_sh + d0);
+    float qq = V::dot(qv, qv, 0.0f);
 #pragma unroll
-      for (int e = 0; e < VEC; e += 4) {
-        f32x4 x = load4(qp + e);
-        qv[e] = x[0]; qv[e + 1] = x[1]; qv[e + 2] = x[2]; qv[e + 3] = x[3];
-        ss += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-      }
-#pragma unroll
-      for (int o = 1; o < LPK; o <<= 1) ss += __shfl_xor(ss, o);
-      const float iq = 1.0f / fmaxf(sqrtf(ss), a.eps);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) qv[e] *= iq;
-    }
+    for (int o = 1; o < LPK; o <<= 1) qq += __shfl_xor(qq, o);
+    const float iq = 1.0f / fmaxf(sqrtf(qq), a.eps);
     const int64_t cend = c0 + kChunk < pos + 1 ? c0 + kChunk : pos + 1;
     const T* kb = (const T*)a.kc + b * a.ks.sb + h * a.ks.sh + d0;
     const T* vb = (const T*)a.vc + b * a.vs.sb + h * a.vs.sh + d0;
     for (int64_t base = c0 + (int64_t)wave * KPW * kDecUnroll; base < cend; base += 4 * KPW * kDecUnroll) {
-      float kv[kDecUnroll][VEC];
-      bool ok[kDecUnroll];
+      vec kv[kDecUnroll];
 #pragma unroll
       for (int u = 0; u < kDecUnroll; ++u) {
         const int64_t j = base + u * KPW + kl;
-        ok[u] = j < cend;
-        const T* kp = kb + (ok[u] ? j : c0) * a.ks.st;
-#pragma unroll
-        for (int e = 0; e < VEC; e += 4) {
-          f32x4 x = load4(kp + e);
-          kv[u][e] = x[0]; kv[u][e + 1] = x[1]; kv[u][e + 2] = x[2]; kv[u][e + 3] = x[3];
-        }
+        kv[u] = *reinterpret_cast<const vec*>(kb + (j < cend ? j : c0) * a.ks.st);
       }
 #pragma unroll
       for (int u = 0; u < kDecUnroll; ++u) {
-        float dot = 0.0f, ss = 0.0f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) { dot += qv[e] * kv[u][e]; ss += kv[u][e] * kv[u][e]; }
+        float dot = V::dot(qv, kv[u], 0.0f), ss = V::dot(kv[u], kv[u], 0.0f);
 #pragma unroll
         for (int o = 1; o < LPK; o <<= 1) { dot += __shfl_xor(dot, o); ss += __shfl_xor(ss, o); }
-        const float s = dot * (1.0f / fmaxf(sqrtf(ss), a.eps));
+        const float s = dot * iq * (1.0f / fmaxf(sqrtf(ss), a.eps));
         const float av = trim(s, hp.r);
         const int64_t j = base + u * KPW + kl;
-        if (ok[u] && av > 0.0f) {
-          const float m = softmask((int)(pos - j), hp.iw);
-          const T* vp = vb + j * a.vs.st;
-          float vv[VEC], vs2 = 0.0f;
-#pragma unroll
-          for (int e = 0; e < VEC; e += 4) {
-            f32x4 x = load4(vp + e);
-            vv[e] = x[0]; vv[e + 1] = x[1]; vv[e + 2] = x[2]; vv[e + 3] = x[3];
-            vs2 += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-          }
+        if (j < cend && av > 0.0f) {
           // every lane of the key's group takes this branch together
+          const float m = softmask((int)(pos - j), hp.iw);
+          const vec vv = *reinterpret_cast<const vec*>(vb + j * a.vs.st);
+          float vs2 = V::dot(vv, vv, 0.0f);
 #pragma unroll
           for (int o = 1; o < LPK; o <<= 1) vs2 += __shfl_xor(vs2, o);
           const float coef = av * av * m / fmaxf(sqrtf(vs2), a.eps);
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[e] += coef * vv[e];
+          for (int e = 0; e < VEC; ++e) acc[e] += coef * V::get(vv, e);
         }
       }
     }
@@ -127,28 +122,43 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
   }
 }
 
+// Sum of the chunk partials in a fixed order (chunk groups c % G, then the
+// groups in order) and TanhNorm; block per (b, h).
 template <typename T, int D>
-__global__ __launch_bounds__(128) void decode_reduce_kernel(DecArgs a) {
-  __shared__ float red[128];
-  const int bh = blockIdx.x;
-  const int d = threadIdx.x;
+__global__ __launch_bounds__(256) void decode_reduce_kernel(DecArgs a) {
+  constexpr int G = 256 / D;  // chunk groups
+  __shared__ float red[256];
+  __shared__ float sq[D];
+  const int bh = blockIdx.x, t = threadIdx.x, d = t % D, g = t / D;
   const HeadParams hp = head_params(a.r, a.w, bh % a.H);
   const int64_t pos = a.len - 1;
   int64_t lo = pos - hp.wc + 1;
   if (lo < 0) lo = 0;
   const int used = (int)((pos - lo + 1 + kChunk - 1) / kChunk);
-  float x = 0.0f;
-  if (d < D)
-    for (int c = 0; c < used; ++c) x += a.part[((int64_t)bh * a.nchunks + c) * D + d];
-  red[d] = x * x;
+  const float* pp = a.part + (int64_t)bh * a.nchunks * D + d;
+  float x0 = 0.0f, x1 = 0.0f;
+  int c = g;
+  for (; c + G < used; c += 2 * G) {
+    x0 += pp[(int64_t)c * D];
+    x1 += pp[(int64_t)(c + G) * D];
+  }
+  if (c < used) x0 += pp[(int64_t)c * D];
+  red[t] = x0 + x1;
   __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (d < s) red[d] += red[d + s];
+  float x = 0.0f;
+  if (t < D) {
+#pragma unroll
+    for (int k = 0; k < G; ++k) x += red[k * D + t];
+    sq[t] = x * x;
+  }
+  __syncthreads();
+  for (int s2 = D / 2; s2 > 0; s2 >>= 1) {
+    if (t < s2) sq[t] += sq[t + s2];
     __syncthreads();
   }
-  const float nc = fmaxf(sqrtf(red[0]), a.eps);
+  const float nc = fmaxf(sqrtf(sq[0]), a.eps);
   const float f = tanhf(nc) / nc;
-  if (d < D) ((T*)a.y)[(int64_t)bh * D + d] = from_f<T>(f * x);
+  if (t < D) ((T*)a.y)[(int64_t)bh * D + t] = from_f<T>(f * x);
 }
 
 int decode_chunk_keys() { return kChunk; }
@@ -161,13 +171,14 @@ static hipError_t launch_decode_t(const DecodeCall& c) {
   a.kc = c.kc; a.ks = c.ks; a.vc = c.vc; a.vs = c.vs;
   a.r = c.r; a.w = c.w; a.part = c.part; a.y = c.y;
   a.H = c.H; a.len = c.len; a.nchunks = c.nchunks; a.eps = c.eps;
+  // the decode timer brackets both kernels: the whole single-query step
   timer_begin(7, c.stream);
   hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3((unsigned)c.nchunks, (unsigned)(c.B * c.H)), dim3(256), 0,
                      c.stream, a);
-  timer_end(7, c.stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_reduce_kernel<T, D>), dim3((unsigned)(c.B * c.H)), dim3(128), 0, c.stream, a);
+  hipLaunchKernelGGL((decode_reduce_kernel<T, D>), dim3((unsigned)(c.B * c.H)), dim3(256), 0, c.stream, a);
+  timer_end(7, c.stream);
   return hipGetLastError();
 }
 

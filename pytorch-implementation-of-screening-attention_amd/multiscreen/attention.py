@@ -107,7 +107,8 @@ class ScreeningAttention(nn.Module):
     # KV-cache inference (no reference counterpart: the reference's
     # MultiscreenLM.generate re-runs forward() on the whole prefix for every
     # token, model.py:111-141).  The cache holds the raw k/v projections
-    # (B, T_cap, H, D); decode(pos) computes exactly row `pos` of forward().
+    # (viewed as (B, T_cap, H, D)); decode(pos) computes exactly row `pos` of
+    # forward().
     # ------------------------------------------------------------------
     def prefill(self, x: torch.Tensor, cache) -> torch.Tensor:
         """Causal self-attention forward over x (B,T,d) at positions 0..T-1;
@@ -135,11 +136,17 @@ class ScreeningAttention(nn.Module):
 
 
 class KVCache:
-    """Raw k/v projections of one attention layer, (B, capacity, H, D)."""
+    """Raw k/v projections of one attention layer.
+
+    Stored head-major, (B, H, capacity, D), so that one head's window is one
+    contiguous stream for the decode kernel; `k` and `v` are the (B, capacity,
+    H, D) views of that storage, the layout of the projections."""
 
     def __init__(self, batch, capacity, num_heads, head_dim, dtype, device):
-        self.k = torch.zeros((batch, capacity, num_heads, head_dim), dtype=dtype, device=device)
-        self.v = torch.zeros_like(self.k)
+        self._k = torch.zeros((batch, num_heads, capacity, head_dim), dtype=dtype, device=device)
+        self._v = torch.zeros_like(self._k)
+        self.k = self._k.permute(0, 2, 1, 3)
+        self.v = self._v.permute(0, 2, 1, 3)
         self.workspace = None
         if self.k.is_cuda:
             from . import _native
