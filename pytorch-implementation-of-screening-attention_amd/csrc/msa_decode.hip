@@ -83,7 +83,8 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
 #pragma unroll
       for (int u = 0; u < kDecUnroll; ++u) {
         const int64_t j = base + u * KPW + kl;
-        kv[u] = *reinterpret_cast<const vec*>(kb + (j < cend ? j : c0) * a.ks.st);
+        // streamed once: non-temporal loads keep the stream from churning the caches
+        kv[u] = __builtin_nontemporal_load(reinterpret_cast<const vec*>(kb + (j < cend ? j : c0) * a.ks.st));
       }
 #pragma unroll
       for (int u = 0; u < kDecUnroll; ++u) {
