@@ -167,11 +167,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   using M = Mma<T>;
   using frag = typename M::frag;
   using S = StageTile<T, DP>;
+  using WS = WaveStage<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  // DMA ring of staged key tiles: NBUF buffers, NBUF-1 tiles ahead
-  constexpr int NBUF = 3 * 2 * S::TILEB <= 100 * 1024 ? 3 : 2;
-  constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile
-  __shared__ __attribute__((aligned(16))) char stage[NBUF][2 * S::TILEB];  // [buffer][K tile | V tile]
+  // per wave: DMA ring of its key half of the live key tiles (K rows | V
+  // rows), NBUF buffers, NBUF-1 tiles ahead; waves never wait for each other
+  // inside the tile loop
+  constexpr int NBUF = 4 * 2 * 2 * WS::TILEB <= 80 * 1024 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) char stage[4][NBUF][2 * WS::TILEB];
+  static_assert(2 * NDH * 16 * kWave * 4 <= 4 * NBUF * 2 * WS::TILEB, "exchange must fit the stage buffers");
   __shared__ __attribute__((aligned(16))) float sk[4][32];                 // per wave: 1/|k| (0 if masked)
   __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v|
   const int tid = threadIdx.x, lane = tid & 63;
@@ -214,8 +217,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
   const int m = perm_row(l32);
   auto stage_tile = [&](int kt, int buf, uint8_t& msk) {
-    S::issue(krow0, a.ks.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf], tid, w);
-    S::issue(vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
+    WS::issue(krow0, a.ks.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf], lane);
+    WS::issue(vrow0, a.vs.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf] + WS::TILEB, lane);
     const int j = kt * kTile + 32 * kh + m;
     msk = (a.kpm != nullptr && j < a.Tk) ? a.kpm[(int64_t)b * a.Tk + j] : (uint8_t)0;
   };
@@ -230,8 +233,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     QueryRows<T, DP> qr;
     qr.load(a, b, h, bh, i, half);
     stage_tile(tl[0], 0, mk[0]);
-    for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
-    if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1, mk[1]);
+    tl[1] = walk.next();
     iql = qr.finish(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
@@ -255,14 +257,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
 
   for (int it = 0; tl[0] >= 0; ++it) {
-    // tile tl[0] is in LDS once this wave's older DMA is done and every wave
-    // passed the barrier; the buffer refilled next was read last iteration
-    if (NBUF == 3 && tl[1] >= 0) wait_vmcnt<PT>();
-    else wait_vmcnt<0>();
-    block_sync_lds();
-    if (tl[NBUF - 1] >= 0) stage_tile(tl[NBUF - 1], (it + NBUF - 1) % NBUF, mk[NBUF - 1]);
-    const char* kl = stage[it % NBUF];
-    const char* vl = kl + S::TILEB;
+    // this wave's DMA of tile tl[0] is complete; with two buffers the other
+    // one (read last iteration, LDS reads done) takes the next tile
+    wait_vmcnt<0>();
+    wave_lds_sync();
+    if (NBUF == 2 && tl[1] >= 0) stage_tile(tl[1], (it + 1) & 1, mk[1]);
+    const char* kl = stage[w][NBUF == 2 ? (it & 1) : 0];
+    const char* vl = kl + WS::TILEB;
     const int cur = tl[0];
     const uint8_t mk_cur = mk[0];
     const int k0 = cur * kTile;
@@ -274,8 +275,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     frag ka[NKS], va[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      ka[ks] = S::frag(kl, 32 * kh + m, ks, half, jok, a.D);
-      va[ks] = S::frag(vl, 32 * kh + m, ks, half, jok, a.D);
+      ka[ks] = S::frag(kl, m, ks, half, jok, a.D);
+      va[ks] = S::frag(vl, m, ks, half, jok, a.D);
     }
     float isk[16], isv[16];
     {
@@ -347,9 +348,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     guard_frags(ka);
     guard_frags(va);
 
-#pragma unroll
-    for (int n = 0; n < NBUF - 1; ++n) { tl[n] = tl[n + 1]; mk[n] = mk[n + 1]; }
-    tl[NBUF - 1] = walk.next();
+    if (NBUF == 1 && tl[1] >= 0) {
+      wave_lds_sync();  // this wave's reads of the single buffer are done
+      stage_tile(tl[1], 0, mk[1]);
+    }
+    tl[0] = tl[1];
+    mk[0] = mk[1];
+    tl[1] = walk.next();
   }
   guard_frags(qb);
   guard_frags(hb);
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   // the kh = 1 wave's accumulator reaches the kh = 0 wave through the
   // (now idle) stage buffers
   __syncthreads();
-  float* red = reinterpret_cast<float*>(&stage[0][0]);  // [qh][NDH][16][64]
+  float* red = reinterpret_cast<float*>(&stage[0][0][0]);  // [qh][NDH][16][64]
   if (kh == 1) {
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk)

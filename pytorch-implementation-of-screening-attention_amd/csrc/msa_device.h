@@ -490,6 +490,33 @@ struct StageTile {
   }
 };
 
+// 32-row half tiles staged global -> LDS by one wave's DMA into its own
+// buffer (no block barrier needed): same row layout and swizzle as StageTile.
+template <typename T, int DP>
+struct WaveStage {
+  using S = StageTile<T, DP>;
+  static constexpr int ROWB = S::ROWB, CPR = S::CPR;
+  static constexpr int TILEB = 32 * ROWB;      // bytes per half tile
+  static constexpr int CPL = 32 * CPR / 64;    // chunks per lane
+  // DMA rows r0 .. r0+31 (row stride st elements; nrows >= 1 valid rows, D
+  // valid columns) into `lds`; rows past the end read the last row, columns
+  // past D the row's first chunk.
+  __device__ static inline void issue(const T* row0, int64_t st, int64_t r0, int64_t nrows, int D, char* lds,
+                                      int lane) {
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int c = u * 64 + lane;
+      const int R = c / CPR, p = c % CPR;
+      int64_t row = r0 + R;
+      if (row > nrows - 1) row = nrows - 1;
+      int col = ((p ^ S::swz(R)) * 16) / (int)sizeof(T);
+      if (col >= D) col = 0;
+      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(row0 + row * st + col),
+                                       (void __attribute__((address_space(3)))*)(lds + u * 64 * 16), 16, 0, 0);
+    }
+  }
+};
+
 // Set bits of a sequence of bitmap positions lo..hi, visited in increasing
 // order 64 at a time through a wave ballot; bit(p) reads position p.  All
 // state is wave-uniform.
