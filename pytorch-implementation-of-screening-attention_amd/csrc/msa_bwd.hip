@@ -216,9 +216,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const T* krow0 = (const T*)a.k + b * a.ks.sb + h * a.ks.sh;
   const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
   const int m = perm_row(l32);
+  const auto plk = WS::plan(a.ks.st, a.D, lane), plv = WS::plan(a.vs.st, a.D, lane);
   auto stage_tile = [&](int kt, int buf, uint8_t& msk) {
-    WS::issue(krow0, a.ks.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf], lane);
-    WS::issue(vrow0, a.vs.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf] + WS::TILEB, lane);
+    WS::issue(plk, krow0, a.ks.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf], lane, 0);
+    WS::issue(plv, vrow0, a.vs.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf] + WS::TILEB, lane, 0);
     const int j = kt * kTile + 32 * kh + m;
     msk = (a.kpm != nullptr && j < a.Tk) ? a.kpm[(int64_t)b * a.Tk + j] : (uint8_t)0;
   };
@@ -247,6 +248,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     for (int ks = 0; ks < NKS; ++ks) *reinterpret_cast<frag*>(dst + KS * ks + PER * half) = hb[ks];
     if (half == 0) a.iqs[(int64_t)bh * a.Tq_pad + i] = valid ? iql : 0.0f;
   }
+  const float thq = hp.thr / iql;  // s > thr  <=>  (q . k)/|k| > thr |q|
   frag id[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
@@ -275,8 +277,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     frag ka[NKS], va[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      ka[ks] = S::frag(kl, m, ks, half, jok, a.D);
-      va[ks] = S::frag(vl, m, ks, half, jok, a.D);
+      ka[ks] = WS::frag(kl, m, ks, half, a.D);
+      va[ks] = WS::frag(vl, m, ks, half, a.D);
     }
     float isk[16], isv[16];
     {
@@ -288,8 +290,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       }
       s2k += __shfl_xor(s2k, 32);
       s2v += __shfl_xor(s2v, 32);
-      const float ik = (jok && mk_cur == 0) ? 1.0f / fmaxf(sqrtf(s2k), a.eps) : 0.0f;
-      const float iv = 1.0f / fmaxf(sqrtf(s2v), a.eps);
+      const float ik = (jok && mk_cur == 0) ? inv_len(s2k, a.eps) : 0.0f;
+      const float iv = inv_len(s2v, a.eps);
       wave_lds_sync();
       if (half == 0) { sk[w][m] = ik; sv[w][m] = iv; }
       wave_lds_sync();
@@ -306,14 +308,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       s = M::mma_ng(ka[ks], qb[ks], s);
       dp = M::mma_ng(va[ks], hb[ks], dp);
     }
-    // pre-square values; register r -> key k0 + 32kh + rowof(r, half), lane -> query i
+    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i.  A
+    // conservative gate on the raw products (s > thr), then the exact test
+    // only for registers where some lane passes; only a quadrant with a pair
+    // past the threshold contributes to dq.
     bool anyp = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = trim(s[r] * isk[r] * iql, hp.r);
-      anyp |= s[r] > 0.0f;
-    }
-    // only a quadrant with a pair past the threshold contributes to dq
+    for (int r = 0; r < 16; ++r) anyp |= s[r] * isk[r] > thq;
     if (__ballot(anyp) != 0ull) {
       frag kta[NDH * NC];  // K^T by identity, packed as the A operand of the dQ product
       {
@@ -327,11 +328,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       const int rel0 = i - (k0 + 32 * kh + 8 * half);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-        const float av = s[r];
         float ds = 0.0f;
-        if (av > 0.0f && valid && in_window(dd, hp.wc, causal))
-          ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+        if (__ballot(s[r] * isk[r] > thq) != 0ull) {
+          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+          const float av = trim(s[r] * isk[r] * iql, hp.r);
+          if (av > 0.0f && valid && in_window(dd, hp.wc, causal))
+            ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+        }
         dp[r] = ds * isk[r];
       }
       // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
@@ -454,9 +457,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const T* qrow0 = (const T*)a.q + b * a.qs.sb + h * a.qs.sh;
   const T* dh0 = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
   const float* iq0 = a.iqs + (int64_t)bh * a.Tq_pad;
+  const auto plq = S::plan(a.qs.st, a.D, tid), plh = S::plan(DP, DP, tid);
   auto stage_tile = [&](int qt, int buf) {
-    S::issue(qrow0, a.qs.st, (int64_t)qt * kTile, a.Tq, a.D, stage[buf], tid, w);
-    S::issue(dh0, DP, (int64_t)qt * kTile, a.Tq_pad, DP, stage[buf] + S::TILEB, tid, w);
+    S::issue(plq, qrow0, a.qs.st, (int64_t)qt * kTile, a.Tq, a.D, stage[buf], tid, w);
+    S::issue(plh, dh0, DP, (int64_t)qt * kTile, a.Tq_pad, DP, stage[buf] + S::TILEB, tid, w);
     if (w == 0)  // 64 floats of 1/|q|: lanes 0-15 carry them, the rest repeat lane 15 into the slot's tail
       __builtin_amdgcn_global_load_lds(
           (const void __attribute__((address_space(1)))*)(iq0 + (int64_t)qt * kTile + 4 * (lane < 16 ? lane : 15)),
@@ -493,6 +497,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     for (int r = 0; r < 16; ++r) { acc_k[dblk][r] = 0.0f; acc_v[dblk][r] = 0.0f; }
   float dr_acc = 0.0f, dw_acc = 0.0f;
   const int m = perm_row(l32);
+  const float thk = hp.thr / ikl;  // s > thr  <=>  (q . k)/|q| > thr |k|  (+inf for masked keys)
 
   if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
   for (int it = 0; tl[0] >= 0; ++it) {
@@ -508,12 +513,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     const int q0 = tl[0] * kTile;
 
     // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
-    const bool iok = q0 + 32 * qh + m < a.Tq;
+    // (rows past Tq carry 1/|q| = 0 and dh = 0, so they contribute nothing)
     frag qa[NKS], ha[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      qa[ks] = S::frag(ql, 32 * qh + m, ks, half, iok, a.D);
-      ha[ks] = S::frag(hl, 32 * qh + m, ks, half, iok, DP);
+      qa[ks] = S::frag(ql, 32 * qh + m, ks, half, a.D);
+      ha[ks] = S::frag(hl, 32 * qh + m, ks, half, DP);
     }
     float isq[16];
     read_row_scales(iql + 32 * qh, half, isq);
@@ -538,30 +543,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       guard_frags(vf);
     }
 
-    // similarities s (in place); register r -> query q0 + 32qh + rowof(r, half),
-    // lane -> key j.  Only a quadrant with a pair past the threshold
-    // contributes to dk, dv, dr, dw.
+    // register r -> query q0 + 32qh + rowof(r, half), lane -> key j.  A
+    // conservative gate on the raw products (s > thr), then the exact test
+    // only for registers where some lane passes; only a quadrant with a pair
+    // past the threshold contributes to dk, dv, dr, dw.
     bool anyp = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = s[r] * isq[r] * ikl;
-      anyp |= trim(s[r], hp.r) > 0.0f;
-    }
+    for (int r = 0; r < 16; ++r) anyp |= s[r] * isq[r] > thk;
     if (__ballot(anyp) != 0ull) {
       const int rel0 = (q0 + 32 * qh + 8 * half) - j;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-        const float sv = s[r];
-        const float av = trim(sv, hp.r);
         float p = 0.0f, ds = 0.0f;
-        if (av > 0.0f && in_window(dd, hp.wc, causal)) {
-          const float mk = softmask(dd, hp.iw);
-          const float g = dp[r] * ivl;
-          p = av * av * mk;
-          ds = 2.0f * av * hp.r * mk * g;
-          dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
-          dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+        if (__ballot(s[r] * isq[r] > thk) != 0ull) {
+          const int dd = rel0 + 16 * (r >> 3) + (r & 7);
+          const float sv = s[r] * isq[r] * ikl;
+          const float av = trim(sv, hp.r);
+          if (av > 0.0f && in_window(dd, hp.wc, causal)) {
+            const float mk = softmask(dd, hp.iw);
+            const float g = dp[r] * ivl;
+            p = av * av * mk;
+            ds = 2.0f * av * hp.r * mk * g;
+            dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
+            dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+          }
         }
         s[r] = p;
         dp[r] = ds * isq[r];

@@ -198,6 +198,8 @@ struct HeadParams {
   float w;     // window w_h > 1
   float iw;    // 1/w
   int wc;      // ceil(w) (capped at 2^30): for integer distance d, d < w  <=>  d < wc
+  float thr;   // 1 - 1/r - 1e-6: s > thr for every pair with 1 - r(1-s) > 0 (a
+               // conservative gate; the exact test follows wherever it passes)
 };
 
 __device__ inline HeadParams head_params(const float* r, const float* w, int h) {
@@ -207,6 +209,7 @@ __device__ inline HeadParams head_params(const float* r, const float* w, int h) 
   p.iw = 1.0f / p.w;
   float c = ceilf(p.w);
   p.wc = c > 1073741824.0f ? 1073741824 : (int)c;
+  p.thr = 1.0f - 1.0f / p.r - 1e-6f;
   return p;
 }
 
@@ -309,50 +312,12 @@ __device__ inline int64_t floordiv(int64_t a, int64_t b) {  // b > 0
   return a >= 0 ? a / b : -((-a + b - 1) / b);
 }
 
-// ---------------------------------------------------------------------------
-// Operand rows.  A lane that supplies row m of an operand holds its NKS slot
-// groups: d = KS*ks + PER*half + e.  Its partner lane (lane ^ 32) holds the
-// other half of the row, so row reductions take one cross-half shuffle.
-// ---------------------------------------------------------------------------
-template <typename T, int DP>
-struct Row {
-  static constexpr int KS = Mma<T>::KS, PER = Mma<T>::PER, NKS = DP / KS, N = NKS * PER;
-  float x[N];
-
-  // Loads the lane's slots of row `p` (D valid columns); zeros when !ok.  `p`
-  // must point at a readable row even when !ok (callers clamp the row index):
-  // every load is issued unconditionally and masked afterwards, so the loads
-  // of several rows can be in flight together.
-  __device__ inline void load(const T* p, bool ok, int D, int half) {
-    typename Mma<T>::frag f[NKS];
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const int d0 = KS * ks + PER * half;
-      f[ks] = Mma<T>::load(p + (d0 < D ? d0 : 0));
-    }
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const bool in = ok && KS * ks + PER * half < D;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) x[ks * PER + e] = in ? Mma<T>::get(f[ks], e) : 0.0f;
-    }
-  }
-  // Full-row dot product with another row held by the same lanes.
-  __device__ inline float dot(const Row& o) const {
-    float s = 0.0f;
-#pragma unroll
-    for (int n = 0; n < N; ++n) s += x[n] * o.x[n];
-    return s + __shfl_xor(s, 32);
-  }
-  __device__ inline float inv_norm(float eps) const { return 1.0f / fmaxf(sqrtf(dot(*this)), eps); }
-  // Operand fragment of slot group ks scaled by c.
-  __device__ inline typename Mma<T>::frag frag(int ks, float c) const {
-    f32x16 t;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) t[e] = x[ks * PER + e] * c;
-    return Mma<T>::pack(t, 0);
-  }
-};
+// 1/max(sqrt(ss), eps) from a squared length, by the hardware reciprocal
+// square root (v_rsq_f32, ~1 ulp): min(rsq(ss), 1/eps) is the same clamp
+// (rsq(0) = +inf).
+__device__ inline float inv_len(float ss, float eps) {
+  return fminf(__builtin_amdgcn_rsqf(ss), __builtin_amdgcn_rcpf(eps));
+}
 
 // Sum of products of two operand fragments in fp32: v_dot2c_f32_bf16 (two
 // exact bf16 products per instruction) for bf16, a plain product for fp32.
@@ -394,7 +359,7 @@ struct PRow {
     for (int ks = 0; ks < NKS; ++ks) s = frag_dot(f[ks], o.f[ks], s);
     return s + __shfl_xor(s, 32);
   }
-  __device__ inline float inv_norm(float eps) const { return 1.0f / fmaxf(sqrtf(dot(*this)), eps); }
+  __device__ inline float inv_norm(float eps) const { return inv_len(dot(*this), eps); }
   // this <- a*this + b*o, rounded to T
   __device__ inline void axpby(float a, float b, const PRow& o) {
 #pragma unroll
@@ -440,20 +405,23 @@ __device__ inline void block_sync_lds() {
 __device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
-// 64-row tiles staged global -> LDS by direct DMA (global_load_lds, 16 bytes a
-// lane, no register round trip) for a 256-thread block.  LDS tile: 64 rows of
-// DP elements, row-major, with the 16-byte chunks of row R XOR-swizzled by
-// swz(R) so that the A-operand reads of 8 consecutive lanes (rows
-// base + {0..3, 8..11} under perm_row) fall in distinct bank groups.
-// Rows past the tensor's end read its last row and columns past D read the
-// row's first chunk (valid memory either way); consumers mask both.
+// Row tiles staged global -> LDS by direct DMA (global_load_lds, 16 bytes a
+// lane, no register round trip).  LDS tile: ROWS rows of DP elements,
+// row-major, with the 16-byte chunks of row R XOR-swizzled by swz(R) so that
+// the A-operand reads of 8 consecutive lanes (rows base + {0..3, 8..11} under
+// perm_row) fall in distinct bank groups.  NT threads (a block, or one wave
+// staging its own half tile) share a tile: thread t moves chunks
+// c = u*NT + t.  The per-thread source offsets are planned once (plan()); a
+// tile that runs past the tensor's last row reads that row instead (slow
+// path, last tile only), and columns past D read the row's first chunk;
+// consumers mask both.
 // ---------------------------------------------------------------------------
-template <typename T, int DP>
+template <typename T, int DP, int ROWS = 64, int NT = 256>
 struct StageTile {
   static constexpr int ROWB = DP * (int)sizeof(T);  // bytes per row
   static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row (4..32)
-  static constexpr int TILEB = 64 * ROWB;           // bytes per tile
-  static constexpr int CPT = 64 * CPR / 256;        // chunks per thread
+  static constexpr int TILEB = ROWS * ROWB;         // bytes per tile
+  static constexpr int CPT = ROWS * CPR / NT;       // chunks per thread
   __device__ static inline int swz(int R) {
     if constexpr (CPR == 4) return ((R >> 1) & 1) | ((R >> 2) & 2);
     else return (R & 3) | ((R >> 1) & 4);
@@ -463,59 +431,65 @@ struct StageTile {
     const int byte = d * (int)sizeof(T);
     return R * ROWB + ((((byte >> 4) ^ swz(R)) << 4) | (byte & 15));
   }
-  // DMA rows r0 .. r0+63 of a tensor whose row r starts at row0 + r*st
-  // (elements; nrows >= 1 rows, D valid columns) into `lds`.  `wave` must be
-  // wave-uniform (the LDS destination of one instruction is a uniform base).
-  __device__ static inline void issue(const T* row0, int64_t st, int64_t r0, int64_t nrows, int D, char* lds,
-                                      int tid, int wave) {
+  __device__ static inline void chunk(int u, int t, int D, int& R, int& col) {
+    const int c = u * NT + t;
+    R = c / CPR;
+    col = (((c % CPR) ^ swz(R)) * 16) / (int)sizeof(T);
+    if (col >= D) col = 0;
+  }
+  // Per-thread element offsets (row R of the tile at R*st) of its chunks.
+  struct Plan {
+    int off[CPT];
+  };
+  __device__ static inline Plan plan(int64_t st, int D, int t) {
+    Plan p;
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int c = u * 256 + tid;
-      const int R = c / CPR, p = c % CPR;
-      int64_t row = r0 + R;
-      if (row > nrows - 1) row = nrows - 1;
-      int col = ((p ^ swz(R)) * 16) / (int)sizeof(T);
-      if (col >= D) col = 0;
-      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(row0 + row * st + col),
-                                       (void __attribute__((address_space(3)))*)(lds + (u * 256 + wave * 64) * 16),
-                                       16, 0, 0);
+      int R, col;
+      chunk(u, t, D, R, col);
+      p.off[u] = (int)(R * st) + col;
+    }
+    return p;
+  }
+  // DMA rows r0 .. r0+ROWS-1 of a tensor whose row r starts at row0 + r*st
+  // (nrows >= 1 rows, D valid columns) into `lds`.  `grp` (wave index for a
+  // block-wide stager, 0 for a wave stager) must be wave-uniform: the LDS
+  // destination of one instruction is a uniform base.
+  __device__ static inline void issue(const Plan& pl, const T* row0, int64_t st, int64_t r0, int64_t nrows, int D,
+                                      char* lds, int t, int grp) {
+    const T* base = row0 + r0 * st;
+    if (r0 + ROWS <= nrows) {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u)
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(base + pl.off[u]),
+                                         (void __attribute__((address_space(3)))*)(lds + (u * NT + grp * 64) * 16),
+                                         16, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) {
+        int R, col;
+        chunk(u, t, D, R, col);
+        const int64_t row = r0 + R < nrows ? R : nrows - 1 - r0;
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(base + row * st + col),
+                                         (void __attribute__((address_space(3)))*)(lds + (u * NT + grp * 64) * 16),
+                                         16, 0, 0);
+      }
     }
   }
-  // A/B operand fragment: row R, slots d = KS*ks + PER*half + e; zero when
-  // the row is invalid or the slots lie past D.
-  __device__ static inline typename Mma<T>::frag frag(const char* lds, int R, int ks, int half, bool row_ok, int D) {
+  // A/B operand fragment: row R, slots d = KS*ks + PER*half + e.  Rows need
+  // no mask here (every consumer zeroes their scale factors or weights);
+  // columns past D exist only when DP = 32 holds D = 16, and read as zero.
+  __device__ static inline typename Mma<T>::frag frag(const char* lds, int R, int ks, int half, int D) {
     const int d0 = Mma<T>::KS * ks + Mma<T>::PER * half;
     const typename Mma<T>::frag f = Mma<T>::load((const T*)(lds + off(R, d0)));
-    return (row_ok && d0 < D) ? f : Mma<T>::zero();
+    if constexpr (DP == 32) return d0 < D ? f : Mma<T>::zero();
+    else return f;
   }
 };
-
-// 32-row half tiles staged global -> LDS by one wave's DMA into its own
-// buffer (no block barrier needed): same row layout and swizzle as StageTile.
+// A wave staging its own 32-row half tile into its own buffer (no block
+// barrier needed).
 template <typename T, int DP>
-struct WaveStage {
-  using S = StageTile<T, DP>;
-  static constexpr int ROWB = S::ROWB, CPR = S::CPR;
-  static constexpr int TILEB = 32 * ROWB;      // bytes per half tile
-  static constexpr int CPL = 32 * CPR / 64;    // chunks per lane
-  // DMA rows r0 .. r0+31 (row stride st elements; nrows >= 1 valid rows, D
-  // valid columns) into `lds`; rows past the end read the last row, columns
-  // past D the row's first chunk.
-  __device__ static inline void issue(const T* row0, int64_t st, int64_t r0, int64_t nrows, int D, char* lds,
-                                      int lane) {
-#pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-      const int c = u * 64 + lane;
-      const int R = c / CPR, p = c % CPR;
-      int64_t row = r0 + R;
-      if (row > nrows - 1) row = nrows - 1;
-      int col = ((p ^ S::swz(R)) * 16) / (int)sizeof(T);
-      if (col >= D) col = 0;
-      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(row0 + row * st + col),
-                                       (void __attribute__((address_space(3)))*)(lds + u * 64 * 16), 16, 0, 0);
-    }
-  }
-};
+using WaveStage = StageTile<T, DP, 32, 64>;
 
 // Set bits of a sequence of bitmap positions lo..hi, visited in increasing
 // order 64 at a time through a wave ballot; bit(p) reads position p.  All

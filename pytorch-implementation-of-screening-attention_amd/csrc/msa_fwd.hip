@@ -403,9 +403,10 @@ void fwd_live_kernel(FwdKArgs a) {
 
   const T* kg = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
   const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
+  const auto plk = S::plan(DP, DP, tid), plv = S::plan(a.vs.st, a.D, tid);
   auto stage_tile = [&](int kt, int buf) {
-    S::issue(kg, DP, (int64_t)kt * kTile, a.Tk_pad, DP, stage[buf], tid, w);
-    S::issue(vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
+    S::issue(plk, kg, DP, (int64_t)kt * kTile, a.Tk_pad, DP, stage[buf], tid, w);
+    S::issue(plv, vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
   };
   // own queries as raw B operands (lane -> query) and 1/|q_i|; their loads go
   // first, the first key tiles' DMA behind them (vector memory returns in order)
@@ -423,6 +424,7 @@ void fwd_live_kernel(FwdKArgs a) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
   }
+  const float thq = hp.thr / iq;  // s > thr  <=>  k^ . q > thr |q|
   frag id[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
@@ -444,15 +446,14 @@ void fwd_live_kernel(FwdKArgs a) {
     const char* vl = kl + S::TILEB;
     const int k0 = tl[0] * kTile;
 
-    // key rows j = k0 + 32*kh + perm_row(l32): K^ (zero past Tk) and raw V
-    // with 1/|v|
+    // key rows j = k0 + 32*kh + perm_row(l32): K^ (zero past Tk, so those
+    // keys never pass the threshold) and raw V with 1/|v|
     const int j = k0 + 32 * kh + m;
-    const bool jok = j < a.Tk;
     frag kf[NKS], va[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      kf[ks] = S::frag(kl, 32 * kh + m, ks, half, true, DP);
-      va[ks] = S::frag(vl, 32 * kh + m, ks, half, jok, a.D);
+      kf[ks] = S::frag(kl, 32 * kh + m, ks, half, DP);
+      va[ks] = S::frag(vl, 32 * kh + m, ks, half, a.D);
     }
     f32x16 s;
 #pragma unroll
@@ -465,15 +466,13 @@ void fwd_live_kernel(FwdKArgs a) {
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) s = M::mma(kf[ks], qf[ks], s);
     }
-    // pre-square values (in place); register r -> key k0 + 32kh + rowof(r, half),
-    // lane -> query i.  Only a quadrant with a pair past the threshold
-    // contributes to h.
+    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i.  A
+    // conservative gate on the raw products (s > thr), then the exact test
+    // only for registers where some lane passes; only a quadrant with a pair
+    // past the threshold contributes to h.
     bool anyp = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = trim(s[r] * iq, hp.r);
-      anyp |= s[r] > 0.0f;
-    }
+    for (int r = 0; r < 16; ++r) anyp |= s[r] > thq;
     if (__ballot(anyp) != 0ull) {
       // 1/|v_j| in register order
       float isv[16];
@@ -482,7 +481,7 @@ void fwd_live_kernel(FwdKArgs a) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) s2 = frag_dot(va[ks], va[ks], s2);
         s2 += __shfl_xor(s2, 32);
-        const float iv = 1.0f / fmaxf(sqrtf(s2), a.eps);
+        const float iv = inv_len(s2, a.eps);
         wave_lds_sync();
         if (half == 0) sv[w][m] = iv;
         wave_lds_sync();
@@ -492,10 +491,12 @@ void fwd_live_kernel(FwdKArgs a) {
       const int rel0 = i - (k0 + 32 * kh + 8 * half);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-        const float av = s[r];
         float p = 0.0f;
-        if (av > 0.0f && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
+        if (__ballot(s[r] > thq) != 0ull) {
+          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+          const float av = trim(s[r] * iq, hp.r);
+          if (av > 0.0f && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
+        }
         s[r] = p;
       }
       // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
