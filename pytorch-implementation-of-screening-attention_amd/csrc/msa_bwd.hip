@@ -183,8 +183,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   int qt, bh;
   xcd_interleave(qt, bh);
   const int b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
+  const HeadParams hp = head_params(a.r, a.w, h, causal);
   const int q0 = qt * kTile;
   const int i = q0 + 32 * qh + l32;
   const bool valid = i < a.Tq;
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
         if (__ballot(s[r] * isk[r] > thq) != 0ull) {
           const int dd = rel0 - (16 * (r >> 3) + (r & 7));
           const float av = trim(s[r] * isk[r] * iql, hp.r);
-          if (av > 0.0f && valid && in_window(dd, hp.wc, causal))
+          if (av > 0.0f && valid && in_window(dd, hp))
             ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
         }
         dp[r] = ds * isk[r];
@@ -417,8 +417,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   int kt, bh;
   xcd_interleave(kt, bh);
   const int b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
+  const HeadParams hp = head_params(a.r, a.w, h, causal);
   const int k0 = kt * kTile;
   const int j = k0 + 32 * kh + l32;
   const bool jvalid = j < a.Tk;
@@ -559,7 +559,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
           const int dd = rel0 + 16 * (r >> 3) + (r & 7);
           const float sv = s[r] * isq[r] * ikl;
           const float av = trim(sv, hp.r);
-          if (av > 0.0f && in_window(dd, hp.wc, causal)) {
+          if (av > 0.0f && in_window(dd, hp)) {
             const float mk = softmask(dd, hp.iw);
             const float g = dp[r] * ivl;
             p = av * av * mk;

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
   __shared__ float red[4][D];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h);
+  const HeadParams hp = head_params(a.r, a.w, h, true);
   const int64_t pos = a.len - 1;
   int64_t lo = pos - hp.wc + 1;
   if (lo < 0) lo = 0;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecArgs a) {
   __shared__ float red[256];
   __shared__ float sq[D];
   const int bh = blockIdx.x, t = threadIdx.x, d = t % D, g = t / D;
-  const HeadParams hp = head_params(a.r, a.w, bh % a.H);
+  const HeadParams hp = head_params(a.r, a.w, bh % a.H, true);
   const int64_t pos = a.len - 1;
   int64_t lo = pos - hp.wc + 1;
   if (lo < 0) lo = 0;

@@ -200,9 +200,15 @@ struct HeadParams {
   int wc;      // ceil(w) (capped at 2^30): for integer distance d, d < w  <=>  d < wc
   float thr;   // 1 - 1/r - 1e-6: s > thr for every pair with 1 - r(1-s) > 0 (a
                // conservative gate; the exact test follows wherever it passes)
+  int wsh;     // window as one unsigned compare: dd in window  <=>
+  unsigned wlim;  // (unsigned)(dd + wsh) < wlim
 };
 
-__device__ inline HeadParams head_params(const float* r, const float* w, int h) {
+// In-window distances dd = i - j (attention.py:111-118 causal, :176-181
+// non-causal): causal 0 <= dd < wc, i.e. shift 0 and limit wc; non-causal
+// -wc < dd < wc, i.e. shift wc-1 and limit 2wc-1.  Positions stay below 2^22
+// and wc <= 2^30, so dd + wsh never overflows.
+__device__ inline HeadParams head_params(const float* r, const float* w, int h, bool causal) {
   HeadParams p;
   p.r = r[h];
   p.w = w[h];
@@ -210,14 +216,13 @@ __device__ inline HeadParams head_params(const float* r, const float* w, int h) 
   float c = ceilf(p.w);
   p.wc = c > 1073741824.0f ? 1073741824 : (int)c;
   p.thr = 1.0f - 1.0f / p.r - 1e-6f;
+  p.wsh = causal ? 0 : p.wc - 1;
+  p.wlim = causal ? (unsigned)p.wc : (unsigned)(2 * p.wc - 1);
   return p;
 }
 
-// In-window test on the integer distance dd = i - j (attention.py:111-118 causal,
-// :176-181 non-causal).  Positions stay below 2^22, so int arithmetic is exact.
-__device__ inline bool in_window(int dd, int wc, bool causal) {
-  return causal ? (dd >= 0 && dd < wc) : (dd < wc && -dd < wc);
-}
+// Branch-free in-window test on the integer distance dd = i - j.
+__device__ inline bool in_window(int dd, const HeadParams& hp) { return (unsigned)(dd + hp.wsh) < hp.wlim; }
 
 // Trim-and-square pre-square value a = 1 - r (1 - s)  (attention.py:90).
 __device__ inline float trim(float s, float r) { return 1.0f - r * (1.0f - s); }

@@ -184,8 +184,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   screen_order(a, bx, bh);
   const int grp = bx / a.nsegl, seg0 = bx % a.nsegl;
   const int b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
+  const HeadParams hp = head_params(a.r, a.w, h, causal);
   const int qt = grp * 4 + wave;
   const bool wave_ok = qt < a.nqt;
   const int q0 = qt * kTile;
@@ -259,13 +259,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma(kf[ks], qf[qh * NKS + ks], acc[qh]);
     }
   };
-  // Threshold vote on key half kh of the tile at k0: a(s) is monotone in s and
-  // s = acc/|q_i| in acc, so the half has a live pair iff its largest
-  // in-window acc passes.  Register r of the half holds key
-  // k0 + 32kh + 16(r/8) + 8half + r%8.
-  auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh) -> bool {
-    const bool interior = causal ? (k0 + 63 <= q0 && q0 + 63 - k0 < hp.wc)
-                                 : (q0 + 63 - k0 < hp.wc && k0 + 63 - q0 < hp.wc);
+  // Threshold vote on key half kh of the tile at k0, per lane (no ballot): a(s)
+  // is monotone in s and s = acc/|q_i|, so the half has a live pair iff its
+  // largest in-window acc passes.  Register r of the half holds key
+  // k0 + 32kh + 16(r/8) + 8half + r%8.  Tiles wholly inside every pair's
+  // window skip the per-register window test.
+  auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh, bool interior) -> bool {
     bool lv = false;
 #pragma unroll
     for (int qh = 0; qh < 2; ++qh) {
@@ -276,68 +275,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       } else {
         const int rel0 = (q0 + 32 * qh + l32) - k0 - 32 * kh - 8 * half;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-          if (in_window(dd, hp.wc, causal)) mx = fmaxf(mx, acc[qh][r]);
-        }
+        for (int r = 0; r < 16; ++r)
+          mx = fmaxf(mx, in_window(rel0 - (16 * (r >> 3) + (r & 7)), hp) ? acc[qh][r] : -INFINITY);
       }
       lv |= trim(mx * iq[qh], hp.r) > 0.0f;
     }
     return lv;
+  };
+  // Tile kt lies wholly inside the window of each of this wave's pairs iff
+  // i - j stays in window at its two extreme corners.
+  auto interior_tile = [&](int kt) {
+    const int d_max = q0 + 63 - kt * kTile, d_min = q0 - kt * kTile - 63;
+    return in_window(d_max, hp) && in_window(d_min, hp);
+  };
+  // Live tiles are rare (a few percent of the window): one lane ORs the bit of
+  // each into the bitmap (cleared by prep_k_kernel), so segments that share a
+  // bitmap word need no ordering.
+  auto finish = [&](int kd, bool lv) {
+    if (__ballot(lv) != 0 && lane == 0) atomicOr(&brow[kd >> 5], 1u << (kd & 31));
   };
 
   for (int sg = seg0;; sg += a.nsegl) {
     const int slo = blo + sg * G::SEG;
     if (slo > bhi) break;
     const int shi = slo + G::SEG - 1 < bhi ? slo + G::SEG - 1 : bhi;
+    // Tiles past shi are replaced by shi itself: the ring slot they fill is
+    // free and never read, and every step then waits for the same count.
 #pragma unroll
-    for (int n = 0; n < NST - 1; ++n)
-      if (slo + n <= shi) issue(slo + n, n);
+    for (int n = 0; n < NST - 1; ++n) issue(slo + n <= shi ? slo + n : shi, n);
 
     // Software pipeline over the two 32-key halves of each tile: the vote on
     // one half runs while the MFMAs of the next half are in flight.  Order in
     // step kt: MFMA(kt, keys 0-31) -> finish tile kt-1 (vote on its keys
     // 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).
-    uint32_t word = 0u;
     f32x16 acc0[2], acc1[2];
-    bool pend = false, live0 = false;  // tile kt-1: keys 32-63 pending in acc1; vote on keys 0-31
+    bool pend = false, live0 = false, pint = false;  // tile kt-1: keys 32-63 pending in acc1
     int pk0 = 0;
-    auto finish = [&](int kd, bool lv) {
-      if (__ballot(lv) != 0) word |= 1u << (kd & 31);
-      if ((kd & 31) == 31 || kd == shi) {
-        if (word != 0u && lane == 0) atomicOr(&brow[kd >> 5], word);
-        word = 0u;
-      }
-    };
     // unrolled by NST so every ring slot offset is a constant
     for (int base = slo; base <= shi; base += NST) {
 #pragma unroll
       for (int u = 0; u < NST; ++u) {
         const int kt = base + u;
         if (kt > shi) break;
-        // tile kt's DMA (own part) is complete when at most the younger
+        // tile kt's DMA (own part) is complete once only the two younger
         // tiles' chunks are outstanding; the barrier then covers all waves
-        const int younger = shi - kt < NST - 2 ? shi - kt : NST - 2;
-        if (younger >= 2) wait_vmcnt<2 * G::CPT>();
-        else if (younger == 1) wait_vmcnt<G::CPT>();
-        else wait_vmcnt<0>();
+        wait_vmcnt<2 * G::CPT>();
         __builtin_amdgcn_s_barrier();
-        if (kt + NST - 1 <= shi) issue(kt + NST - 1, (u + NST - 1) % NST);
+        issue(kt + NST - 1 <= shi ? kt + NST - 1 : shi, (u + NST - 1) % NST);
 
         const bool mine = kt >= kt_lo && kt <= kt_hi;
         const char* slot = ring + u * G::TILEB;
         if (mine) half_mma(slot, 0, acc0);
-        if (kt > slo) finish(kt - 1, pend && (live0 || vote_half(acc1, pk0, 1)));
+        if (kt > slo) finish(kt - 1, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
         if (mine) {
           half_mma(slot, 1, acc1);
-          live0 = vote_half(acc0, kt * kTile, 0);
+          pint = interior_tile(kt);
+          live0 = vote_half(acc0, kt * kTile, 0, pint);
           pk0 = kt * kTile;
         }
         pend = mine;
       }
     }
-    finish(shi, pend && (live0 || vote_half(acc1, pk0, 1)));
-    // every wave is done with the ring before the next segment refills it
+    finish(shi, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
+    // the replacement loads are done and every wave is done with the ring
+    // before the next segment refills it
+    wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
   }
   guard_frags(qf);
@@ -374,8 +376,8 @@ void fwd_live_kernel(FwdKArgs a) {
   int qt, bh;
   xcd_interleave(qt, bh);
   const int b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h);
   const bool causal = a.causal != 0;
+  const HeadParams hp = head_params(a.r, a.w, h, causal);
   const int q0 = qt * kTile;
   const int i = q0 + 32 * qh + l32;
   const bool valid = i < a.Tq;
@@ -495,7 +497,7 @@ void fwd_live_kernel(FwdKArgs a) {
         if (__ballot(s[r] > thq) != 0ull) {
           const int dd = rel0 - (16 * (r >> 3) + (r & 7));
           const float av = trim(s[r] * iq, hp.r);
-          if (av > 0.0f && in_window(dd, hp.wc, causal)) p = av * av * softmask(dd, hp.iw) * isv[r];
+          if (av > 0.0f && in_window(dd, hp)) p = av * av * softmask(dd, hp.iw) * isv[r];
         }
         s[r] = p;
       }
