@@ -409,12 +409,30 @@ __device__ inline void block_sync_lds() {
 // memory operations across the point (LDS ops of one wave run in order).
 __device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// XOR swizzle of the 16-byte chunk positions of LDS row R (rows of CPR
+// chunks).  A ds_read_b128 whose lanes read rows perm_row(l%32) at one chunk
+// position is conflict-free if the rows a bank window serves land in distinct
+// 16-byte bank groups, whether the LDS serves 8 lanes (128 bytes) or 16 lanes
+// (256 bytes) a cycle: 8 lanes read rows {0..3, 8..11} (+4, +16), 16 lanes
+// rows 0..15 (+16).  With bits b0..b3 of R:
+//   CPR 4  (2 rows per 128 B): (b1^b2, b3) is one-to-one on the rows sharing
+//          b0 in either set of rows, and on those sharing (b0, b1) in 0..15;
+//   CPR 8  (1 row per 128 B) : (b1, b3, b0^b2) is one-to-one on {0..3, 8..11}
+//          and on {4..7, 12..15}, and on the even and the odd rows of 0..15;
+//   CPR>=16: (b1, b3, b0^b2, b0) is also one-to-one on all of 0..15.
+template <int CPR>
+__device__ inline int lds_swz(int R) {
+  const int b0 = R & 1, b1 = (R >> 1) & 1, b2 = (R >> 2) & 1, b3 = (R >> 3) & 1;
+  if constexpr (CPR == 4) return (b1 ^ b2) | (b3 << 1);
+  else if constexpr (CPR == 8) return b1 | (b3 << 1) | ((b0 ^ b2) << 2);
+  else return b1 | (b3 << 1) | ((b0 ^ b2) << 2) | (b0 << 3);
+}
+
 // ---------------------------------------------------------------------------
 // Row tiles staged global -> LDS by direct DMA (global_load_lds, 16 bytes a
 // lane, no register round trip).  LDS tile: ROWS rows of DP elements,
-// row-major, with the 16-byte chunks of row R XOR-swizzled by swz(R) so that
-// the A-operand reads of 8 consecutive lanes (rows base + {0..3, 8..11} under
-// perm_row) fall in distinct bank groups.  NT threads (a block, or one wave
+// row-major, with the 16-byte chunks of row R XOR-swizzled by lds_swz (below)
+// so that operand reads under perm_row are free of bank conflicts.  NT threads (a block, or one wave
 // staging its own half tile) share a tile: thread t moves chunks
 // c = u*NT + t.  The per-thread source offsets are planned once (plan()); a
 // tile that runs past the tensor's last row reads that row instead (slow
@@ -427,10 +445,7 @@ struct StageTile {
   static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row (4..32)
   static constexpr int TILEB = ROWS * ROWB;         // bytes per tile
   static constexpr int CPT = ROWS * CPR / NT;       // chunks per thread
-  __device__ static inline int swz(int R) {
-    if constexpr (CPR == 4) return ((R >> 1) & 1) | ((R >> 2) & 2);
-    else return (R & 3) | ((R >> 1) & 4);
-  }
+  __device__ static inline int swz(int R) { return lds_swz<CPR>(R); }
   // byte offset of element d of row R
   __device__ static inline int off(int R, int d) {
     const int byte = d * (int)sizeof(T);

@@ -117,13 +117,9 @@ struct ScreenTile {
   static constexpr int CPT = 64 * CPR / 256;         // DMA chunks per thread per tile
   static constexpr int NST = 4;                      // pipeline stages (3 tiles in flight)
   static constexpr int SEG = 256;                    // key tiles per work segment
-  // LDS chunk position of global chunk c of row R: c ^ swz(R).  A ds_read_b128
-  // of 8 consecutive lanes touches rows base + {0..3, 8..11} (perm_row) at one
-  // chunk; swz makes those 8 reads hit distinct 16-byte bank groups.
-  __device__ static inline int swz(int R) {
-    if constexpr (CPR == 4) return ((R >> 1) & 1) | ((R >> 2) & 2);
-    else return (R & 3) | ((R >> 1) & 4);
-  }
+  // LDS chunk position of global chunk c of row R: c ^ swz(R), conflict-free
+  // for the perm_row operand reads
+  __device__ static inline int swz(int R) { return lds_swz<CPR>(R); }
 };
 constexpr int kScreenSegBlocks = 8;  // max blocks per query-tile group
 
