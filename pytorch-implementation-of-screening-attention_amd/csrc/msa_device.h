@@ -346,8 +346,8 @@ struct PRow {
   static constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS;
   frag f[NKS];
 
-  // Same contract as Row::load: `p` readable even when !ok; unconditional
-  // loads, masked afterwards.
+  // `p` must be readable even when !ok: the loads are unconditional and
+  // masked afterwards.
   __device__ inline void load(const T* p, bool ok, int D, int half) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {

@@ -80,24 +80,6 @@ struct FwdKArgs {
   float eps;
 };
 
-// Loads Q^T B-operand fragments (raw values) and 1/|q| for the 64 queries of
-// tile qt: lane -> query q0 + 32*qh + l32, slots -> d.
-template <typename T, int DP>
-__device__ inline void load_q_tile(const FwdKArgs& a, int b, int h, int q0, bool wave_ok, int half, int l32,
-                                   typename Mma<T>::frag (&qf)[2 * (DP / Mma<T>::KS)], float (&iq)[2]) {
-  constexpr int NKS = DP / Mma<T>::KS;
-#pragma unroll
-  for (int qh = 0; qh < 2; ++qh) {
-    const int i = q0 + 32 * qh + l32;
-    const bool ok = wave_ok && i < a.Tq;
-    PRow<T, DP> row;
-    row.load((const T*)a.q + b * a.qs.sb + (int64_t)(ok ? i : 0) * a.qs.st + h * a.qs.sh, ok, a.D, half);
-    iq[qh] = row.inv_norm(a.eps);
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = row.f[ks];
-  }
-}
-
 // Key-tile range [lo, hi] of the window of queries [qa, qb].
 __device__ inline void key_tile_range(const FwdKArgs& a, const HeadParams& hp, bool causal, int64_t qa, int64_t qb,
                                       int& lo, int& hi) {
@@ -142,10 +124,10 @@ __device__ inline void screen_order(const FwdKArgs& a, int& bx, int& bh) {
   const int jh = s / nx;                                 // this XCD's jh-th head
   const int k = 8 * jh + ((jh & 1) ? 7 - x : x);         // its rank, widest first
   const int lane = threadIdx.x & 63;
-  const float wl = lane < BH ? a.w[lane % a.H] : 0.0f;
+  const float wl = lane < BH ? a.w[lane % a.H] : 0.0f;  // lane o holds head o's window
   int rank = 0;
   for (int o = 0; o < BH; ++o) {
-    const float wo = a.w[o % a.H];
+    const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), o));
     rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
   }
   bh = __builtin_ctzll(__ballot(lane < BH && rank == k));
@@ -195,9 +177,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   }
   if (blo + seg0 * G::SEG > bhi) return;  // block-uniform: no segment for this block
 
+  // own query rows (raw B operands); their 1/|q| is formed once the first
+  // key tiles' DMA is in flight behind them
+  PRow<T, DP> qrow[2];
+#pragma unroll
+  for (int qh = 0; qh < 2; ++qh) {
+    const int i = q0 + 32 * qh + l32;
+    const bool ok = wave_ok && i < a.Tq;
+    qrow[qh].load((const T*)a.q + b * a.qs.sb + (int64_t)(ok ? i : 0) * a.qs.st + h * a.qs.sh, ok, a.D, half);
+  }
   frag qf[2 * NKS];
   float iq[2];
-  load_q_tile<T, DP>(a, b, h, q0, wave_ok, half, l32, qf, iq);
   uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + (wave_ok ? qt : 0)) * a.nkt_words;
 
   // DMA: chunk c = u*256 + tid of a tile (row c / CPR, LDS position c % CPR)
@@ -291,14 +281,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     if (__ballot(lv) != 0 && lane == 0) atomicOr(&brow[kd >> 5], 1u << (kd & 31));
   };
 
+  // Tiles past a segment's last tile shi are replaced by shi itself: the ring
+  // slot they fill is free and never read, and every step then waits for the
+  // same count.
+  auto prologue = [&](int slo, int shi) {
+#pragma unroll
+    for (int n = 0; n < NST - 1; ++n) issue(slo + n <= shi ? slo + n : shi, n);
+  };
+  auto seg_end = [&](int slo) { return slo + G::SEG - 1 < bhi ? slo + G::SEG - 1 : bhi; };
+  prologue(blo + seg0 * G::SEG, seg_end(blo + seg0 * G::SEG));
+#pragma unroll
+  for (int qh = 0; qh < 2; ++qh) {
+    iq[qh] = qrow[qh].inv_norm(a.eps);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = qrow[qh].f[ks];
+  }
+
   for (int sg = seg0;; sg += a.nsegl) {
     const int slo = blo + sg * G::SEG;
     if (slo > bhi) break;
-    const int shi = slo + G::SEG - 1 < bhi ? slo + G::SEG - 1 : bhi;
-    // Tiles past shi are replaced by shi itself: the ring slot they fill is
-    // free and never read, and every step then waits for the same count.
-#pragma unroll
-    for (int n = 0; n < NST - 1; ++n) issue(slo + n <= shi ? slo + n : shi, n);
+    const int shi = seg_end(slo);
+    if (sg != seg0) prologue(slo, shi);
 
     // Software pipeline over the two 32-key halves of each tile: the vote on
     // one half runs while the MFMAs of the next half are in flight.  Order in

@@ -144,10 +144,18 @@ def test_backward_deterministic():
         assert torch.equal(a, b)
 
 
-def test_tile_bitmap_matches_oracle_counts():
-    B, T, H, D = 1, 640, 4, 64
+# Screen work distribution: B*H = 4 uses one work queue; 8 uses eight queues
+# with heads ranked by window; 72 uses eight queues without ranking; T = 2048
+# with wide windows cuts each query group's key range into several parts.
+@pytest.mark.parametrize("B,T,H,r,w", [
+    (1, 640, 4, [1.1, 1.3, 1.6, 2.0], [100.0, 250.5, 640.0, 1e5]),
+    (2, 640, 4, [1.1, 1.3, 1.6, 2.0], [100.0, 250.5, 640.0, 1e5]),
+    (9, 192, 8, [1.2] * 8, [30.0, 60.0, 90.0, 120.0, 150.0, 180.0, 1e4, 2.0]),
+    (1, 2048, 8, [1.1, 1.2, 1.3, 1.4, 1.5, 1.6, 1.8, 2.0], [1e5, 3000.0, 1700.0, 900.0, 2048.0, 64.0, 1e5, 500.0]),
+], ids=["bh4", "bh8", "bh72", "t2048"])
+def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
+    D = 64
     q, k, v = correlated_qkv(B, T, T, H, D, seed=4, dtype=torch.float32, rho=0.3)
-    r, w = [1.1, 1.3, 1.6, 2.0], [100.0, 250.5, 640.0, 1e5]
     y, hnorm, bits = _run_fwd(q, k, v, r, w, True)
     nW, nA, act = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True)
     nqt = nkt = T // 64
