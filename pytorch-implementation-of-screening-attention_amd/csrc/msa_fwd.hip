@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // each into the bitmap (cleared by prep_k_kernel), so segments that share a
   // bitmap word need no ordering.
   auto finish = [&](int kd, bool lv) {
-    if (__ballot(lv) != 0 && lane == 0) atomicOr(&brow[kd >> 5], 1u << (kd & 31));
+    if (__ballot(lv) != 0 && wave_ok && lane == 0) atomicOr(&brow[kd >> 5], 1u << (kd & 31));
   };
 
   // Tiles past a segment's last tile shi are replaced by shi itself: the ring
@@ -306,35 +306,66 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     // Software pipeline over the two 32-key halves of each tile: the vote on
     // one half runs while the MFMAs of the next half are in flight.  Order in
     // step kt: MFMA(kt, keys 0-31) -> finish tile kt-1 (vote on its keys
-    // 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).
+    // 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).  Tile kt sits
+    // in ring slot (kt - slo) % NST.
     f32x16 acc0[2], acc1[2];
     bool pend = false, live0 = false, pint = false;  // tile kt-1: keys 32-63 pending in acc1
     int pk0 = 0;
-    // unrolled by NST so every ring slot offset is a constant
-    for (int base = slo; base <= shi; base += NST) {
-#pragma unroll
-      for (int u = 0; u < NST; ++u) {
-        const int kt = base + u;
-        if (kt > shi) break;
-        // tile kt's DMA (own part) is complete once only the two younger
-        // tiles' chunks are outstanding; the barrier then covers all waves
-        wait_vmcnt<2 * G::CPT>();
-        __builtin_amdgcn_s_barrier();
-        issue(kt + NST - 1 <= shi ? kt + NST - 1 : shi, (u + NST - 1) % NST);
-
-        const bool mine = kt >= kt_lo && kt <= kt_hi;
-        const char* slot = ring + u * G::TILEB;
-        if (mine) half_mma(slot, 0, acc0);
-        if (kt > slo) finish(kt - 1, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
-        if (mine) {
-          half_mma(slot, 1, acc1);
-          pint = interior_tile(kt);
-          live0 = vote_half(acc0, kt * kTile, 0, pint);
-          pk0 = kt * kTile;
-        }
-        pend = mine;
+    auto enter = [&](int kt) -> const char* {
+      // tile kt's DMA (own part) is complete once only the two younger tiles'
+      // chunks are outstanding; the barrier then covers all waves
+      wait_vmcnt<2 * G::CPT>();
+      __builtin_amdgcn_s_barrier();
+      const int n = kt - slo;
+      issue(kt + NST - 1 <= shi ? kt + NST - 1 : shi, (n + NST - 1) & (NST - 1));
+      return ring + (n & (NST - 1)) * G::TILEB;
+    };
+    // General step: tiles at the window's edges, or outside some wave's window.
+    auto step = [&](int kt) {
+      const char* slot = enter(kt);
+      const bool mine = kt >= kt_lo && kt <= kt_hi;
+      if (mine) half_mma(slot, 0, acc0);
+      if (kt > slo) finish(kt - 1, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
+      if (mine) {
+        half_mma(slot, 1, acc1);
+        pint = interior_tile(kt);
+        live0 = vote_half(acc0, kt * kTile, 0, pint);
+        pk0 = kt * kTile;
       }
+      pend = mine;
+    };
+    // Straight-line step for tiles wholly inside every valid wave's window,
+    // whose predecessor kt-1 was one as well: plain maxima, no branches but
+    // the rare live-tile store.  A wave past the last query tile has zero
+    // query rows, so its votes fail.
+    auto step_inside = [&](int kt) {
+      const char* slot = enter(kt);
+      half_mma(slot, 0, acc0);
+      finish(kt - 1, pend & (live0 | vote_half(acc1, 0, 1, true)));
+      half_mma(slot, 1, acc1);
+      live0 = vote_half(acc0, 0, 0, true);
+      pend = true;
+      pint = true;
+      pk0 = kt * kTile;
+    };
+    // Tiles [ia, ib] lie inside the window of every valid wave of the block:
+    // from the last valid wave's first interior tile to the first wave's last.
+    int ia, ib;
+    {
+      const int last = (a.nqt - 1 - grp * 4 < 3 ? a.nqt - 1 - grp * 4 : 3);
+      const int64_t qa = (int64_t)(grp * 4 + last) * kTile, qb = (int64_t)grp * 4 * kTile;
+      auto fdiv = [](int64_t x) { return (int)(x >= 0 ? x / kTile : -((-x + kTile - 1) / kTile)); };
+      ia = fdiv(qa + 2 * kTile - 1 - hp.wc);                                   // d_max = qa + 63 - k0 < wc
+      ib = causal ? (int)(qb / kTile) - 1 : fdiv(qb - kTile + (int64_t)hp.wc);  // d_min >= 0, or > -wc
+      if (ia < slo) ia = slo;
+      if (ib > shi) ib = shi;
     }
+    int kt = slo;
+    if (ia < ib) {
+      for (; kt <= ia; ++kt) step(kt);
+      for (; kt <= ib; ++kt) step_inside(kt);
+    }
+    for (; kt <= shi; ++kt) step(kt);
     finish(shi, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
     // the replacement loads are done and every wave is done with the ring
     // before the next segment refills it
