@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // live tile get y = 0, |h| = 0.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 2 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1)))
 void fwd_live_kernel(FwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
@@ -411,7 +411,9 @@ void fwd_live_kernel(FwdKArgs a) {
   const int q0 = qt * kTile;
   const int i = q0 + 32 * qh + l32;
   const bool valid = i < a.Tq;
-  T* yrow = (T*)a.y + (((int64_t)b * a.Tq + (valid ? i : 0)) * a.H + h) * a.D;
+  // output row of query i (formed where it is stored, so nothing holds it
+  // across the tile loop)
+  auto yrow = [&]() { return (T*)a.y + (((int64_t)b * a.Tq + (valid ? i : 0)) * a.H + h) * a.D; };
 
   int kt_lo, kt_hi;
   key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
@@ -427,7 +429,7 @@ void fwd_live_kernel(FwdKArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = 32 * dblk + 8 * g + 4 * half;
-          if (d < a.D) store4(yrow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+          if (d < a.D) store4(yrow() + d, 0.0f, 0.0f, 0.0f, 0.0f);
         }
     }
     return;
@@ -588,7 +590,7 @@ void fwd_live_kernel(FwdKArgs a) {
   const float f = tanhf(nc) / nc;
   if (valid) {
     if (half == 0) a.hnorm[(int64_t)bh * a.Tq + i] = n;
-    store_creg_row<T, NDH>(yrow, a.D, half, [&](int dblk, int r) { return f * o[dblk][r]; });
+    store_creg_row<T, NDH>(yrow(), a.D, half, [&](int dblk, int r) { return f * o[dblk][r]; });
   }
 }
 
