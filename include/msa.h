@@ -26,6 +26,20 @@
  *   r, w    : fp32 (H,), r = exp(s_r)+1, w = exp(s_v)+1 (attention.py:164-165).
  *   key_padding_mask : nullable uint8 (B, Tk), nonzero = ignore key.
  *   dtype   : MSA_F32 or MSA_BF16 for q,k,v,y,dy,dq,dk,dv.
+ *   dropout_p, dropout_seed : attention dropout on alpha*m (attention.py:68,
+ *             :190, nn.Dropout in training mode), 0 <= p < 1; p = 0 is the
+ *             identity.  The keep decision of pair (b, h, i, j) is a
+ *             counter-based hash, so forward and backward agree without
+ *             storing a mask: with key = (b*H+h) << 44 | i << 22 | j and
+ *             z = dropout_seed + key * 0x9E3779B97F4A7C15 (mod 2^64), the
+ *             SplitMix64 finaliser
+ *               z = (z ^ z>>30) * 0xBF58476D1CE4E5B9
+ *               z = (z ^ z>>27) * 0x94D049BB133111EB
+ *               z =  z ^ z>>31
+ *             keeps the pair iff (z >> 32) >= min(floor(p * 2^32), 2^32-1),
+ *             and a kept pair is scaled by 1/(1-p) (fp32).  The reference
+ *             draws its mask from torch's generator, so only the statistics
+ *             match it (keep rate 1-p, unbiased in expectation).
  *
  * Ownership: the caller allocates every buffer (outputs and workspaces); the
  * library never allocates or frees device memory.  Every call is
@@ -82,8 +96,8 @@ size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
  *   _ScreeningFunc.forward / screening_attention_fwd
  *                         attention_triton.py:31-36, screening_fwd.py:216-270
  *   TanhNorm + merge      attention_triton.py:135-137
- * and adds key_padding_mask (attention.py:185-188), which the Triton path
- * ignores (attention_triton.py:125-132).
+ * and adds key_padding_mask (attention.py:185-188) and attention dropout
+ * (attention.py:190), which the Triton path ignores (attention_triton.py:125-132).
  * Outputs: y (B,Tq,H,D) = TanhNorm(h); hnorm (B,H,Tq) fp32 = |h_i| before the
  * eps clamp (needed by msa_bwd); tile_bits (msa_tile_bits_words words).
  */
@@ -92,7 +106,7 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
             const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
             int B, int H, int Tq, int Tk, int D, int dtype,
             const float* r, const float* w, const uint8_t* key_padding_mask,
-            int causal, float eps,
+            int causal, float eps, float dropout_p, uint64_t dropout_seed,
             void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words,
             void* workspace, size_t workspace_bytes, void* stream);
 
@@ -103,8 +117,9 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
  * reference fused path, which returns None for them (attention_triton.py:44)
  * -- produces the per-head gradients dr, dw (H,) that attention.py's autograd
  * delivers to s_r / s_v through r = exp(s_r)+1, w = exp(s_v)+1.
- * Inputs: the forward's q, k, v, r, w, key_padding_mask, causal, eps and its
- * outputs y, hnorm, tile_bits; dy (B,Tq,H,D) contiguous.
+ * Inputs: the forward's q, k, v, r, w, key_padding_mask, causal, eps,
+ * dropout_p, dropout_seed and its outputs y, hnorm, tile_bits; dy (B,Tq,H,D)
+ * contiguous.
  * dq (B,Tq,H,D), dk, dv (B,Tk,H,D) are written in full (zeros where no
  * active pair reaches a row).  Deterministic: no atomics.
  */
@@ -113,7 +128,7 @@ int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
             const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
             int B, int H, int Tq, int Tk, int D, int dtype,
             const float* r, const float* w, const uint8_t* key_padding_mask,
-            int causal, float eps,
+            int causal, float eps, float dropout_p, uint64_t dropout_seed,
             const void* y, const float* hnorm, const void* dy,
             const uint32_t* tile_bits, size_t tile_bits_words,
             void* dq, void* dk, void* dv, float* dr, float* dw,

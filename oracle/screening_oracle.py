@@ -13,6 +13,8 @@ A float64 numpy restatement of the reference's dense algorithm,
   softmask        attention.py:92-119   causal:  (cos(pi(j-i)/w)+1)/2 on -w<j-i<=0
                   attention.py:174-183  non-causal: same on |j-i| < w
   key padding     attention.py:185-188  alpha[b,:,:,j] = 0 where mask
+  dropout         attention.py:190      alpha*m * keep/(1-p), keep from the
+                                        counter-based hash of include/msa.h
   aggregate       attention.py:192-193  h = alpha v^   (no normaliser)
   TanhNorm        norm.py:23-25         tanh(n)/n h,  n = max(|h|, eps)
   per-head params attention.py:164-165  w = exp(s_v)+1, r = exp(s_r)+1
@@ -69,6 +71,47 @@ def softmask_dw(qpos, kpos, w, causal):
     return d * inside
 
 
+_M64 = (1 << 64) - 1
+_PHI, _MIX1, _MIX2 = 0x9E3779B97F4A7C15, 0xBF58476D1CE4E5B9, 0x94D049BB133111EB
+
+
+def dropout_keep_bits(seed, bh, i, j):
+    """Top 32 bits of the SplitMix64 finaliser (Steele, Lea and Flood, OOPSLA
+    2014) of seed + key * 0x9E3779B97F4A7C15 mod 2^64, key = bh << 44 | i << 22
+    | j -- the counter-based dropout hash that include/msa.h defines.  Array
+    arguments broadcast (numpy uint64, wrapping)."""
+    bh, i, j = (np.asarray(x, dtype=np.uint64) for x in (bh, i, j))
+    with np.errstate(over="ignore"):   # arithmetic mod 2^64 is the definition
+        key = (bh << np.uint64(44)) | (i << np.uint64(22)) | j
+        z = np.uint64(seed & _M64) + key * np.uint64(_PHI)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(_MIX1)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(_MIX2)
+        z = z ^ (z >> np.uint64(31))
+    return (z >> np.uint64(32)).astype(np.uint64)
+
+
+def dropout_threshold(p):
+    """Keep threshold min(floor(p * 2^32), 2^32 - 1) of the fp32 probability p."""
+    return min(math.floor(float(np.float32(p)) * 4294967296.0), 4294967295)
+
+
+def dropout_scale(p):
+    """1/(1-p) as the kernels form it, in fp32."""
+    return float(np.float32(1.0) / (np.float32(1.0) - np.float32(p)))
+
+
+def dropout_factor(dropout, B, H, qpos, kpos):
+    """(B,H,len(qpos),len(kpos)) float64: 0 for dropped pairs, 1/(1-p) for kept
+    ones (attention.py:190, nn.Dropout in training mode), for dropout = (p,
+    seed); None when dropout is None or p = 0."""
+    if dropout is None or float(dropout[0]) == 0.0:
+        return None
+    p, seed = dropout
+    bh = (np.arange(B)[:, None] * H + np.arange(H)[None, :]).reshape(B, H, 1, 1)
+    bits = dropout_keep_bits(seed, bh, np.asarray(qpos).reshape(1, 1, -1, 1), np.asarray(kpos).reshape(1, 1, 1, -1))
+    return np.where(bits >= np.uint64(dropout_threshold(p)), dropout_scale(p), 0.0)
+
+
 def _heads(x):
     """(B,T,H,D) -> (B,H,T,D) float64."""
     return np.ascontiguousarray(np.transpose(np.asarray(x, dtype=np.float64), (0, 2, 1, 3)))
@@ -80,10 +123,11 @@ def _blocks(T, block):
 
 
 def forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=None, block=256,
-            q_offset=0, return_h=False):
+            q_offset=0, return_h=False, dropout=None):
     """TanhNorm'd attention output y (B,Tq,H,D); optionally also h (B,H,Tq,D).
 
     Query row t sits at position q_offset + t (0 in the reference forward).
+    dropout = (p, seed): alpha*m times dropout_factor (attention.py:190).
     """
     qn, kn, vn = normalize(_heads(q), eps), normalize(_heads(k), eps), normalize(_heads(v), eps)
     B, H, Tq, D = qn.shape
@@ -96,6 +140,9 @@ def forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=None, block=25
         p = trim_and_square(s, r) * softmask(np.arange(i0, i1) + q_offset, kpos, w, causal)[None]
         if key_padding_mask is not None:
             p = p * (~np.asarray(key_padding_mask, dtype=bool))[:, None, None, :]
+        c = dropout_factor(dropout, B, H, np.arange(i0, i1) + q_offset, kpos)
+        if c is not None:
+            p = p * c
         h[:, :, i0:i1] = p @ vn
     n = np.sqrt(np.sum(h * h, axis=-1, keepdims=True))
     nc = np.maximum(n, eps)
@@ -125,7 +172,7 @@ def _normalize_bwd(x, dxn, eps):
     return np.where(big, (dxn - xn * proj) / np.maximum(n, eps), dxn / eps)
 
 
-def backward(q, k, v, r, w, dy, causal=True, eps=EPS, key_padding_mask=None, block=256):
+def backward(q, k, v, r, w, dy, causal=True, eps=EPS, key_padding_mask=None, block=256, dropout=None):
     """Gradients (dq, dk, dv, dr, dw) of sum(y * dy) for y = forward(...)."""
     qh, kh, vh = _heads(q), _heads(k), _heads(v)
     qn, kn, vn = normalize(qh, eps), normalize(kh, eps), normalize(vh, eps)
@@ -137,7 +184,7 @@ def backward(q, k, v, r, w, dy, causal=True, eps=EPS, key_padding_mask=None, blo
     if key_padding_mask is not None:
         keep = (~np.asarray(key_padding_mask, dtype=bool))[:, None, None, :]
 
-    _, h = forward(q, k, v, r, w, causal, eps, key_padding_mask, block, return_h=True)
+    _, h = forward(q, k, v, r, w, causal, eps, key_padding_mask, block, return_h=True, dropout=dropout)
     g = _heads(dy)
     # TanhNorm backward (norm.py:24-25 with the clamp at eps)
     n = np.sqrt(np.sum(h * h, axis=-1, keepdims=True))
@@ -162,6 +209,10 @@ def backward(q, k, v, r, w, dy, causal=True, eps=EPS, key_padding_mask=None, blo
         if keep is not None:
             m = m * keep
             mdw = mdw * keep
+        c = dropout_factor(dropout, B, H, qpos, kpos)
+        if c is not None:   # every term is linear in the mask factor
+            m = m * c
+            mdw = mdw * c
         p = a * a * m
         dP = dh[:, :, i0:i1] @ np.swapaxes(vn, -1, -2)
         dvn += np.swapaxes(p, -1, -2) @ dh[:, :, i0:i1]
@@ -177,7 +228,15 @@ def backward(q, k, v, r, w, dy, causal=True, eps=EPS, key_padding_mask=None, blo
     return t(dq), t(dk), t(dv), dr, dw
 
 
-def brute_force_forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=None):
+def _keep_bits_int(seed, bh, i, j):
+    """dropout_keep_bits with Python integers (an independent restatement)."""
+    z = (seed + ((bh << 44) | (i << 22) | j) * _PHI) & _M64
+    z = ((z ^ (z >> 30)) * _MIX1) & _M64
+    z = ((z ^ (z >> 27)) * _MIX2) & _M64
+    return (z ^ (z >> 31)) >> 32
+
+
+def brute_force_forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=None, dropout=None):
     """Pure-Python per-pair loops; tiny inputs only.  Same contract as forward()."""
     q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
     B, Tq, H, D = q.shape
@@ -206,6 +265,9 @@ def brute_force_forward(q, k, v, r, w, causal=True, eps=EPS, key_padding_mask=No
                     s = sum(qi[e] * ks[j][e] for e in range(D))
                     a = max(1.0 - float(r[hh]) * (1.0 - s), 0.0)
                     wt = a * a * 0.5 * (math.cos(math.pi * rel / ww) + 1.0)
+                    if dropout is not None and float(dropout[0]) > 0.0:
+                        kept = _keep_bits_int(int(dropout[1]), b * H + hh, i, j) >= dropout_threshold(dropout[0])
+                        wt *= dropout_scale(dropout[0]) if kept else 0.0
                     for e in range(D):
                         acc[e] += wt * vs[j][e]
                 n = max(math.sqrt(sum(e * e for e in acc)), eps)

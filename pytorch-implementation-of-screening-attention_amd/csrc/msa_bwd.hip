@@ -66,6 +66,7 @@ struct BwdKArgs {
   int B, H, Tq, Tk, D, nqt, nkt, nkt_words, causal;
   int64_t Tq_pad;
   float eps;
+  Dropout drop;
 };
 
 // Query-side rows for row i of head (b,h), in two steps so that other memory
@@ -332,8 +333,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
         if (__ballot(s[r] * isk[r] > thq) != 0ull) {
           const int dd = rel0 - (16 * (r >> 3) + (r & 7));
           const float av = trim(s[r] * isk[r] * iql, hp.r);
-          if (av > 0.0f && valid && in_window(dd, hp))
+          if (av > 0.0f && valid && in_window(dd, hp)) {
             ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+            if (a.drop.on) ds *= dropout_factor(a.drop, bh, i, i - dd);
+          }
         }
         dp[r] = ds * isk[r];
       }
@@ -560,12 +563,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
           const float sv = s[r] * isq[r] * ikl;
           const float av = trim(sv, hp.r);
           if (av > 0.0f && in_window(dd, hp)) {
-            const float mk = softmask(dd, hp.iw);
+            const float c = a.drop.on ? dropout_factor(a.drop, bh, j + dd, j) : 1.0f;
+            const float mk = softmask(dd, hp.iw) * c;
             const float g = dp[r] * ivl;
             p = av * av * mk;
             ds = 2.0f * av * hp.r * mk * g;
             dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
-            dw_acc += av * av * g * softmask_dw(dd, hp.iw);
+            dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
           }
         }
         s[r] = p;
@@ -703,6 +707,7 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   ka.nqt = g.nqt; ka.nkt = g.nkt; ka.nkt_words = g.nkt_words; ka.causal = g.causal;
   ka.Tq_pad = g.Tq_pad;
   ka.eps = c.eps;
+  ka.drop = c.drop;
   timer_begin(5, c.stream);
   hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
   timer_end(5, c.stream);

@@ -1,6 +1,7 @@
 // C ABI of libmsa.so (declared in include/msa.h): argument validation on the
 // host, workspace carving, then stream-ordered kernel launches.  No device
 // memory is allocated here.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -10,6 +11,7 @@
 #include <vector>
 
 #include "../../include/msa.h"
+
 #include "msa_internal.h"
 
 namespace {
@@ -177,15 +179,27 @@ size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype) {
   return msa::bwd_ws_bytes(g);
 }
 
+// Keep threshold min(floor(p * 2^32), 2^32-1) and scale 1/(1-p) of dropout p.
+static msa::Dropout dropout_of(float p, uint64_t seed) {
+  msa::Dropout d;
+  d.seed = seed;
+  const double t = floor((double)p * 4294967296.0);
+  d.thresh = t >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)t;
+  d.scale = 1.0f / (1.0f - p);
+  d.on = p > 0.0f ? 1 : 0;
+  return d;
+}
+
 int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_st,
             int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int Tq, int Tk,
             int D, int dtype, const float* r, const float* w, const uint8_t* key_padding_mask, int causal, float eps,
-            void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words, void* workspace,
+            float dropout_p, uint64_t dropout_seed, void* y, float* hnorm, uint32_t* tile_bits, size_t tile_bits_words, void* workspace,
             size_t workspace_bytes, void* stream) {
   msa::Geometry g;
   int rc = check_geometry(B, H, Tq, Tk, D, dtype, causal, &g);
   if (rc != MSA_OK) return rc;
   if (!(eps > 0.0f)) return fail(MSA_ERR_INVALID, "eps must be positive");
+  if (!(dropout_p >= 0.0f && dropout_p < 1.0f)) return fail(MSA_ERR_INVALID, "dropout_p must be in [0, 1)");
   if (B == 0 || Tq == 0) return ok();
   if ((rc = check_tensor("q", q, q_sb, q_st, q_sh, dtype)) != MSA_OK) return rc;
   if (Tk > 0) {
@@ -210,6 +224,7 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
   c.k = k; c.ks = {k_sb, k_st, k_sh};
   c.v = v; c.vs = {v_sb, v_st, v_sh};
   c.r = r; c.w = w; c.kpm = key_padding_mask; c.eps = eps;
+  c.drop = dropout_of(dropout_p, dropout_seed);
   c.y = y; c.hnorm = hnorm; c.bits = tile_bits;
   c.khat = workspace;
   c.stream = (hipStream_t)stream;
@@ -219,13 +234,14 @@ int msa_fwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
 int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_st,
             int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int Tq, int Tk,
             int D, int dtype, const float* r, const float* w, const uint8_t* key_padding_mask, int causal, float eps,
-            const void* y, const float* hnorm, const void* dy, const uint32_t* tile_bits, size_t tile_bits_words,
+            float dropout_p, uint64_t dropout_seed, const void* y, const float* hnorm, const void* dy, const uint32_t* tile_bits, size_t tile_bits_words,
             void* dq, void* dk, void* dv, float* dr, float* dw, void* workspace, size_t workspace_bytes,
             void* stream) {
   msa::Geometry g;
   int rc = check_geometry(B, H, Tq, Tk, D, dtype, causal, &g);
   if (rc != MSA_OK) return rc;
   if (!(eps > 0.0f)) return fail(MSA_ERR_INVALID, "eps must be positive");
+  if (!(dropout_p >= 0.0f && dropout_p < 1.0f)) return fail(MSA_ERR_INVALID, "dropout_p must be in [0, 1)");
   if (dr == nullptr || dw == nullptr) return fail(MSA_ERR_INVALID, "dr and dw must be device arrays of H floats");
   if (B == 0 || Tq == 0 || Tk == 0)
     return fail(MSA_ERR_INVALID, "msa_bwd needs B, Tq, Tk > 0 (the caller zero-fills empty gradients)");
@@ -253,6 +269,7 @@ int msa_bwd(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void*
   c.k = k; c.ks = {k_sb, k_st, k_sh};
   c.v = v; c.vs = {v_sb, v_st, v_sh};
   c.r = r; c.w = w; c.kpm = key_padding_mask; c.eps = eps;
+  c.drop = dropout_of(dropout_p, dropout_seed);
   c.y = y; c.hnorm = hnorm; c.dy = dy; c.bits = tile_bits;
   c.workspace = workspace;
   c.dq = dq; c.dk = dk; c.dv = dv; c.dr = dr; c.dw = dw;

@@ -74,6 +74,7 @@ struct FwdKArgs {
   const void* khat;
   const float* r; const float* w;
   void* y; float* hnorm; uint32_t* bits;
+  Dropout drop;
   int H, Tq, Tk, D, nqt, nkt_words, causal;
   int nsegl;  // screen blocks per 4-query-tile group (segment stride)
   int64_t Tk_pad;
@@ -529,7 +530,10 @@ void fwd_live_kernel(FwdKArgs a) {
         if (__ballot(s[r] > thq) != 0ull) {
           const int dd = rel0 - (16 * (r >> 3) + (r & 7));
           const float av = trim(s[r] * iq, hp.r);
-          if (av > 0.0f && in_window(dd, hp)) p = av * av * softmask(dd, hp.iw) * isv[r];
+          if (av > 0.0f && in_window(dd, hp)) {
+            p = av * av * softmask(dd, hp.iw) * isv[r];
+            if (a.drop.on) p *= dropout_factor(a.drop, bh, i, i - dd);
+          }
         }
         s[r] = p;
       }
@@ -618,7 +622,7 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   fa.q = c.q; fa.qs = c.qs; fa.v = c.v; fa.vs = c.vs; fa.khat = c.khat;
   fa.r = c.r; fa.w = c.w; fa.y = c.y; fa.hnorm = c.hnorm; fa.bits = c.bits;
   fa.H = g.H; fa.Tq = g.Tq; fa.Tk = g.Tk; fa.D = g.D; fa.nqt = g.nqt; fa.nkt_words = g.nkt_words;
-  fa.causal = g.causal; fa.Tk_pad = g.Tk_pad; fa.eps = c.eps;
+  fa.causal = g.causal; fa.Tk_pad = g.Tk_pad; fa.eps = c.eps; fa.drop = c.drop;
   {
     const int nseg = (g.nkt + ScreenTile<T, DP>::SEG - 1) / ScreenTile<T, DP>::SEG;
     fa.nsegl = nseg < kScreenSegBlocks ? (nseg > 0 ? nseg : 1) : kScreenSegBlocks;

@@ -31,6 +31,29 @@ size_t fwd_ws_bytes(const Geometry& g);
 // ([b*h][Tq_pad] fp32) that dq_kernel hands to dkdv_kernel.
 size_t bwd_ws_bytes(const Geometry& g);
 
+// Attention dropout on alpha*m: pair (b, h, i, j) is kept iff the top 32 bits
+// of its hash reach `thresh`, and kept pairs are scaled by `scale` = 1/(1-p).
+struct Dropout {
+  uint64_t seed;
+  uint32_t thresh;
+  float scale;
+  int on;  // p > 0
+};
+
+// Dropout factor of pair (b*H+h, i, j): 0 or d.scale.  The SplitMix64
+// finaliser (Steele, Lea and Flood, "Fast splittable pseudorandom number
+// generators", OOPSLA 2014) of seed + key * 0x9E3779B97F4A7C15, key =
+// bh << 44 | i << 22 | j (bh < 2^16, i, j < 2^22), decides: kept iff its top
+// 32 bits reach d.thresh.
+__device__ inline float dropout_factor(const Dropout& d, int bh, int i, int j) {
+  const uint64_t key = ((uint64_t)(uint32_t)bh << 44) | ((uint64_t)(uint32_t)i << 22) | (uint64_t)(uint32_t)j;
+  uint64_t z = d.seed + key * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return (uint32_t)(z >> 32) >= d.thresh ? d.scale : 0.0f;
+}
+
 struct FwdCall {
   Geometry g;
   const void* q; Strides3 qs;
@@ -38,6 +61,7 @@ struct FwdCall {
   const void* v; Strides3 vs;
   const float* r; const float* w; const uint8_t* kpm;
   float eps;
+  Dropout drop;
   void* y; float* hnorm; uint32_t* bits;
   void* khat;
   hipStream_t stream;
@@ -51,6 +75,7 @@ struct BwdCall {
   const void* v; Strides3 vs;
   const float* r; const float* w; const uint8_t* kpm;
   float eps;
+  Dropout drop;
   const void* y; const float* hnorm; const void* dy;
   const uint32_t* bits;
   void* workspace;

@@ -23,6 +23,7 @@ _p = ctypes.c_void_p
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
 _f = ctypes.c_float
+_u64 = ctypes.c_uint64
 _sz = ctypes.c_size_t
 
 _SIGS = {
@@ -32,10 +33,10 @@ _SIGS = {
     "msa_tile_bits_words": (_sz, [_i, _i, _i, _i]),
     "msa_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "msa_fwd": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
-                     _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _f,
+                     _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _f, _f, _u64,
                      _p, _p, _p, _sz, _p, _sz, _p]),
     "msa_bwd": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
-                     _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _f,
+                     _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _f, _f, _u64,
                      _p, _p, _p, _p, _sz,
                      _p, _p, _p, _p, _p, _p, _sz, _p]),
     "msa_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),

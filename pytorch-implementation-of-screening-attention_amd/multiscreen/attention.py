@@ -79,8 +79,11 @@ class ScreeningAttention(nn.Module):
         dropping = self.training and self.attn_dropout.p > 0.0
         if q.is_cuda:
             if dropping:
-                raise NotImplementedError(
-                    "attention dropout (p>0 in training mode) is not implemented in the fused GPU kernels")
+                # keep mask from a counter-based hash of this seed (drawn from
+                # torch's default generator, so torch.manual_seed reproduces it)
+                seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+                return ops.screening_core(q, k, v, r, w, self.causal, self.eps, key_padding_mask,
+                                          self.attn_dropout.p, seed)
             return ops.screening_core(q, k, v, r, w, self.causal, self.eps, key_padding_mask)
         return screening_core_dense(q, k, v, r, w, self.causal, self.eps, key_padding_mask,
                                     self.attn_dropout if dropping else None)

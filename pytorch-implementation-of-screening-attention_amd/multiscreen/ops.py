@@ -55,10 +55,19 @@ def _kpm_u8(key_padding_mask, B, Tk, dev):
     return key_padding_mask.to(device=dev, dtype=torch.uint8).contiguous()
 
 
-def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None):
+def _dropout_args(dropout_p, seed):
+    p = float(dropout_p)
+    if not 0.0 <= p < 1.0:
+        raise ValueError(f"dropout probability must be in [0, 1), got {p}")
+    return p, int(seed) & (2 ** 64 - 1)
+
+
+def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, dropout_p=0.0, seed=0):
     """One msa_fwd call.  Returns (y, hnorm, tile_bits).
 
     q (B,Tq,H,D), k/v (B,Tk,H,D) in float32 or bfloat16 on one GPU; r, w (H,).
+    dropout_p / seed: attention dropout with the counter-based keep mask that
+    include/msa.h defines (p = 0: none).
     """
     L = _native.lib()
     if not q.is_cuda:
@@ -78,6 +87,7 @@ def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None):
     r32 = r.detach().to(device=dev, dtype=torch.float32).contiguous()
     w32 = w.detach().to(device=dev, dtype=torch.float32).contiguous()
     kpm = _kpm_u8(key_padding_mask, B, Tk, dev)
+    p, seed = _dropout_args(dropout_p, seed)
     y = torch.empty((B, Tq, H, D), dtype=q.dtype, device=dev)
     hnorm = torch.empty((B, H, Tq), dtype=torch.float32, device=dev)
     nwords = tile_bits_words(B, H, Tq, Tk)
@@ -86,15 +96,16 @@ def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None):
     ws = torch.empty((max(wsb, 16),), dtype=torch.uint8, device=dev)
     rc = L.msa_fwd(*_args_bthd(q), *_args_bthd(k), *_args_bthd(v),
                    B, H, Tq, Tk, D, dt, r32.data_ptr(), w32.data_ptr(),
-                   kpm.data_ptr() if kpm is not None else None, int(bool(causal)), float(eps),
+                   kpm.data_ptr() if kpm is not None else None, int(bool(causal)), float(eps), p, seed,
                    y.data_ptr(), hnorm.data_ptr(), bits.data_ptr(), nwords,
                    ws.data_ptr(), wsb, _stream_ptr(dev))
     _native.check(rc, "msa_fwd")
     return y, hnorm, bits
 
 
-def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, dy, key_padding_mask=None):
-    """One msa_bwd call.  Returns (dq, dk, dv, dr, dw); dq/dk/dv in (B,T,H,D)."""
+def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, dy, key_padding_mask=None, dropout_p=0.0, seed=0):
+    """One msa_bwd call.  Returns (dq, dk, dv, dr, dw); dq/dk/dv in (B,T,H,D).
+    dropout_p / seed must be the forward's."""
     L = _native.lib()
     dt = _DTYPES[q.dtype]
     es = q.element_size()
@@ -113,11 +124,12 @@ def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, dy, key_padding_mask=Non
     r32 = r.detach().to(device=dev, dtype=torch.float32).contiguous()
     w32 = w.detach().to(device=dev, dtype=torch.float32).contiguous()
     kpm = _kpm_u8(key_padding_mask, B, Tk, dev)
+    p, seed = _dropout_args(dropout_p, seed)
     wsb = int(L.msa_bwd_workspace_bytes(B, H, Tq, Tk, D, dt))
     ws = torch.empty((max(wsb, 16),), dtype=torch.uint8, device=dev)
     rc = L.msa_bwd(*_args_bthd(q), *_args_bthd(k), *_args_bthd(v),
                    B, H, Tq, Tk, D, dt, r32.data_ptr(), w32.data_ptr(),
-                   kpm.data_ptr() if kpm is not None else None, int(bool(causal)), float(eps),
+                   kpm.data_ptr() if kpm is not None else None, int(bool(causal)), float(eps), p, seed,
                    y.data_ptr(), hnorm.data_ptr(), dy.data_ptr(), bits.data_ptr(),
                    tile_bits_words(B, H, Tq, Tk),
                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dr.data_ptr(), dw.data_ptr(),
@@ -130,28 +142,31 @@ class ScreeningCoreFunction(torch.autograd.Function):
     """Autograd wrapper: forward = msa_fwd, backward = msa_bwd."""
 
     @staticmethod
-    def forward(ctx, q, k, v, r, w, causal, eps, key_padding_mask):
-        y, hnorm, bits = fwd_raw(q, k, v, r, w, causal, eps, key_padding_mask)
+    def forward(ctx, q, k, v, r, w, causal, eps, key_padding_mask, dropout_p=0.0, seed=0):
+        y, hnorm, bits = fwd_raw(q, k, v, r, w, causal, eps, key_padding_mask, dropout_p, seed)
         if any(ctx.needs_input_grad[:5]):
             ctx.save_for_backward(q, k, v, r, w, y, hnorm, bits, key_padding_mask)
         ctx.causal = causal
         ctx.eps = eps
+        ctx.dropout = (dropout_p, seed)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         q, k, v, r, w, y, hnorm, bits, kpm = ctx.saved_tensors
-        dq, dk, dv, dr, dw = bwd_raw(q, k, v, r, w, ctx.causal, ctx.eps, y, hnorm, bits, dy, kpm)
-        return dq, dk, dv, dr.to(r.dtype), dw.to(w.dtype), None, None, None
+        dq, dk, dv, dr, dw = bwd_raw(q, k, v, r, w, ctx.causal, ctx.eps, y, hnorm, bits, dy, kpm, *ctx.dropout)
+        return dq, dk, dv, dr.to(r.dtype), dw.to(w.dtype), None, None, None, None, None
 
 
-def screening_core(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None):
-    """Fused screening attention core; see the module docstring."""
+def screening_core(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, dropout_p=0.0, seed=0):
+    """Fused screening attention core; see the module docstring.  dropout_p > 0
+    applies attention dropout (attention.py:190) with the keep mask of `seed`."""
     if q.dtype == torch.float16:
         # no fp16 kernels: compute in fp32 and return fp16
-        out = ScreeningCoreFunction.apply(q.float(), k.float(), v.float(), r, w, causal, eps, key_padding_mask)
+        out = ScreeningCoreFunction.apply(q.float(), k.float(), v.float(), r, w, causal, eps, key_padding_mask,
+                                          dropout_p, seed)
         return out.to(torch.float16)
-    return ScreeningCoreFunction.apply(q, k, v, r, w, causal, eps, key_padding_mask)
+    return ScreeningCoreFunction.apply(q, k, v, r, w, causal, eps, key_padding_mask, dropout_p, seed)
 
 
 def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None):

@@ -53,12 +53,12 @@ def test_version_and_sizes():
 def _fwd(L, **kw):
     a = dict(q=16, qs=(1024, 64, 8), k=16, ks=(1024, 64, 8), v=16, vs=(1024, 64, 8),
              B=1, H=8, Tq=16, Tk=16, D=8 * 8, dtype=1, r=16, w=16, kpm=None, causal=1, eps=1e-8,
-             y=16, hnorm=16, bits=16, nbits=8, ws=16, wsb=1 << 30, stream=None)
+             drop=0.0, seed=0, y=16, hnorm=16, bits=16, nbits=8, ws=16, wsb=1 << 30, stream=None)
     a["D"] = 64
     a.update(kw)
     return L.msa_fwd(a["q"], *a["qs"], a["k"], *a["ks"], a["v"], *a["vs"], a["B"], a["H"], a["Tq"],
                      a["Tk"], a["D"], a["dtype"], a["r"], a["w"], a["kpm"], a["causal"], a["eps"],
-                     a["y"], a["hnorm"], a["bits"], a["nbits"], a["ws"], a["wsb"], a["stream"])
+                     a["drop"], a["seed"], a["y"], a["hnorm"], a["bits"], a["nbits"], a["ws"], a["wsb"], a["stream"])
 
 
 @pytest.mark.parametrize("kw,code,msg", [
@@ -71,6 +71,8 @@ def _fwd(L, **kw):
     (dict(nbits=0), 2, "tile_bits"),
     (dict(wsb=100), 2, "workspace"),
     (dict(eps=0.0), 1, "eps"),
+    (dict(drop=1.0), 1, "dropout_p"),
+    (dict(drop=-0.1), 1, "dropout_p"),
     (dict(B=70000, H=1), 1, "B*H"),
     (dict(Tq=-1), 1, "negative"),
 ])
@@ -90,10 +92,10 @@ def test_fwd_empty_batch_is_a_no_op():
 
 def test_bwd_and_decode_reject_bad_arguments():
     L = _native.lib()
-    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8,
+    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8, 0.0, 0,
                    16, 16, 16, 16, 1, 16, 16, 16, 16, 16, 16, 10, None)
     assert rc == 2 and "backward workspace" in L.msa_last_error().decode()
-    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8,
+    rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8, 0.0, 0,
                    16, 16, 16, 16, 0, 16, 16, 16, 16, 16, 16, 1 << 20, None)
     assert rc == 2 and "tile_bits" in L.msa_last_error().decode()
     rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 0, 100, 16, 16,

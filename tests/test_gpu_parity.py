@@ -127,6 +127,75 @@ def test_backward_parity(case, dtype):
         assert e <= tol, f"{name}: rel err {e:.3e} > {tol}"
 
 
+# Attention dropout (attention.py:190): the kernels and the oracle share the
+# counter-based keep mask of include/msa.h, so they agree to the usual
+# tolerances; cases 1-3 cover ragged T, key padding and Tq != Tk.
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("ci", [0, 1, 2, 3])
+def test_dropout_parity(ci, dtype):
+    case = FWD_CASES[ci]
+    B, Tq, Tk, H, D, causal, r, w, use_kpm = case
+    q, k, v, kpm = _case_inputs(case, dtype, seed=4)
+    dy = torch.randn(B, Tq, H, D, generator=torch.Generator().manual_seed(9)).to(dtype)
+    drop = (0.3, 0x5EED0000ABCD1234 + ci)
+    ops = _ops()
+    rg, wg = _rw(H, r, w)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kpm_d = None if kpm is None else kpm.to(DEV)
+    y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, kpm_d, *drop)
+    grads = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dy.to(DEV), kpm_d, *drop)
+    torch.cuda.synchronize()
+    kpm_np = None if kpm is None else kpm.numpy()
+    args = (np64(q), np64(k), np64(v), np.array(r), np.array(w))
+    yref = O.forward(*args, causal, key_padding_mask=kpm_np, dropout=drop)
+    ref = O.backward(*args, np64(dy), causal, key_padding_mask=kpm_np, dropout=drop)
+    tol = TOL[dtype]
+    assert rel_err(np64(y), yref) <= tol
+    # the mask is not the identity on this case
+    y0 = O.forward(*args, causal, key_padding_mask=kpm_np)
+    assert np.max(np.abs(yref - y0)) > 1e-3 * np.max(np.abs(y0))
+    for name, got, want in zip(("dq", "dk", "dv", "dr", "dw"), grads, ref):
+        assert np.max(np.abs(want)) > 0, f"{name} vacuous"
+        e = rel_err(np64(got), want)
+        assert e <= tol, f"{name}: rel err {e:.3e} > {tol}"
+
+
+def test_dropout_zero_is_identity_and_seed_reproduces():
+    case = FWD_CASES[1]
+    B, Tq, Tk, H, D, causal, r, w, _ = case
+    q, k, v, _ = _case_inputs(case, torch.bfloat16, seed=5)
+    ops = _ops()
+    rg, wg = _rw(H, r, w)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    base = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None)[0]
+    assert torch.equal(ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None, 0.0, 12345)[0], base)
+    a = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None, 0.5, 777)[0]
+    b = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None, 0.5, 777)[0]
+    c = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None, 0.5, 778)[0]
+    assert torch.equal(a, b) and not torch.equal(a, c)
+
+
+def test_module_dropout_in_training_mode():
+    from multiscreen.attention import ScreeningAttention
+    torch.manual_seed(0)
+    m = ScreeningAttention(128, 2, dropout=0.25).to(DEV)
+    with torch.no_grad():
+        m.s_r.fill_(math.log(0.05))  # r = 1.05: most in-window pairs pass the threshold
+    x = torch.randn(2, 96, 128, device=DEV)
+    m.train()
+    torch.manual_seed(11)
+    y1 = m(x, x, x)
+    torch.manual_seed(11)
+    y2 = m(x, x, x)
+    y3 = m(x, x, x)
+    assert y1.abs().max() > 1e-3
+    assert torch.equal(y1, y2) and not torch.equal(y1, y3)
+    y1.sum().backward()
+    assert m.s_r.grad is not None and torch.isfinite(m.q_proj.weight.grad).all()
+    m.eval()
+    assert torch.equal(m(x, x, x), m(x, x, x))
+
+
 def test_backward_deterministic():
     case = FWD_CASES[0]
     q, k, v, kpm = _case_inputs(case, torch.bfloat16, seed=2)
