@@ -164,7 +164,7 @@ constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
 // wave hands its accumulator to the kh = 0 wave through LDS, which finishes dq.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1))) void dq_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   using S = StageTile<T, DP>;
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   // per wave: DMA ring of its key half of the live key tiles (K rows | V
   // rows), NBUF buffers, NBUF-1 tiles ahead; waves never wait for each other
   // inside the tile loop
-  constexpr int NBUF = 4 * 2 * 2 * WS::TILEB <= 80 * 1024 ? 2 : 1;
+  constexpr int NBUF = 1;  // a small LDS footprint leaves room for three blocks per CU
   __shared__ __attribute__((aligned(16))) char stage[4][NBUF][2 * WS::TILEB];
   static_assert(2 * NDH * 16 * kWave * 4 <= 4 * NBUF * 2 * WS::TILEB, "exchange must fit the stage buffers");
   __shared__ __attribute__((aligned(16))) float sk[4][32];                 // per wave: 1/|k| (0 if masked)
@@ -217,10 +217,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const T* krow0 = (const T*)a.k + b * a.ks.sb + h * a.ks.sh;
   const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
   const int m = perm_row(l32);
-  const auto plk = WS::plan(a.ks.st, a.D, lane), plv = WS::plan(a.vs.st, a.D, lane);
+  // the DMA offsets are formed at each issue from a laundered lane index, so
+  // the compiler keeps no per-lane offsets live across the tile loop
   auto stage_tile = [&](int kt, int buf, uint8_t& msk) {
-    WS::issue(plk, krow0, a.ks.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf], lane, 0);
-    WS::issue(plv, vrow0, a.vs.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf] + WS::TILEB, lane, 0);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const auto plk = WS::plan(a.ks.st, a.D, ln), plv = WS::plan(a.vs.st, a.D, ln);
+    WS::issue(plk, krow0, a.ks.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf], ln, 0);
+    WS::issue(plv, vrow0, a.vs.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf] + WS::TILEB, ln, 0);
     const int j = kt * kTile + 32 * kh + m;
     msk = (a.kpm != nullptr && j < a.Tk) ? a.kpm[(int64_t)b * a.Tk + j] : (uint8_t)0;
   };
@@ -250,9 +254,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     if (half == 0) a.iqs[(int64_t)bh * a.Tq_pad + i] = valid ? iql : 0.0f;
   }
   const float thq = hp.thr / iql;  // s > thr  <=>  (q . k)/|k| > thr |q|
-  frag id[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
   f32x16 adq[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
@@ -260,111 +261,128 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
 
   for (int it = 0; tl[0] >= 0; ++it) {
-    // this wave's DMA of tile tl[0] is complete; with two buffers the other
-    // one (read last iteration, LDS reads done) takes the next tile
+    // this wave's DMA of tile tl[0] is complete
     wait_vmcnt<0>();
     wave_lds_sync();
-    if (NBUF == 2 && tl[1] >= 0) stage_tile(tl[1], (it + 1) & 1, mk[1]);
-    const char* kl = stage[w][NBUF == 2 ? (it & 1) : 0];
+    const char* kl = stage[w][0];
     const char* vl = kl + WS::TILEB;
-    const int cur = tl[0];
+    const int k0 = tl[0] * kTile;
     const uint8_t mk_cur = mk[0];
-    const int k0 = cur * kTile;
 
-    // key rows j = k0 + 32*kh + perm_row(l32) as A operands, with 1/|k|
-    // (0 if padded or masked) and 1/|v|
+    // key rows j = k0 + 32*kh + perm_row(l32) as A operands.  S^T = K Q^T and
+    // dP^T = V dH^T take one operand set at a time (fragments re-read from
+    // LDS when needed again), with the rows' squared norms from the same
+    // fragments.
     const int j = k0 + 32 * kh + m;
     const bool jok = j < a.Tk;
-    frag ka[NKS], va[NKS];
+    f32x16 s, dp;
+    float s2k = 0.0f, s2v = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      ka[ks] = WS::frag(kl, m, ks, half, a.D);
-      va[ks] = WS::frag(vl, m, ks, half, a.D);
-    }
-    float isk[16], isv[16];
+    for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
     {
-      float s2k = 0.0f, s2v = 0.0f;
+      frag f[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) f[ks] = WS::frag(kl, m, ks, half, a.D);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        s2k = frag_dot(ka[ks], ka[ks], s2k);
-        s2v = frag_dot(va[ks], va[ks], s2v);
+        s = M::mma_ng(f[ks], qb[ks], s);
+        s2k = frag_dot(f[ks], f[ks], s2k);
       }
-      s2k += __shfl_xor(s2k, 32);
-      s2v += __shfl_xor(s2v, 32);
-      const float ik = (jok && mk_cur == 0) ? inv_len(s2k, a.eps) : 0.0f;
+      guard_frags(f);
+    }
+    {
+      frag f[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) f[ks] = WS::frag(vl, m, ks, half, a.D);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        dp = M::mma_ng(f[ks], hb[ks], dp);
+        s2v = frag_dot(f[ks], f[ks], s2v);
+      }
+      guard_frags(f);
+    }
+    s2k += __shfl_xor(s2k, 32);
+    s2v += __shfl_xor(s2v, 32);
+    {
+      const float ik = (jok && mk_cur == 0) ? inv_len(s2k, a.eps) : 0.0f;  // 0 if padded or masked
       const float iv = inv_len(s2v, a.eps);
       wave_lds_sync();
       if (half == 0) { sk[w][m] = ik; sv[w][m] = iv; }
       wave_lds_sync();
-      read_row_scales(sk[w], half, isk);
-      read_row_scales(sv[w], half, isv);
     }
-
-    // S^T = K Q^T, dP^T = V dH^T
-    f32x16 s, dp;
+    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i.  Scaled
+    // in place: s = (q . k)/|k|, dp = dH . v^.
+    {
+      float sc[16];
+      read_row_scales(sk[w], half, sc);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
+      for (int r = 0; r < 16; ++r) s[r] *= sc[r];
+      read_row_scales(sv[w], half, sc);
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      s = M::mma_ng(ka[ks], qb[ks], s);
-      dp = M::mma_ng(va[ks], hb[ks], dp);
+      for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
     }
-    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i.  A
-    // conservative gate on the raw products (s > thr), then the exact test
+    // A conservative gate on the products (s > thr |q|), then the exact test
     // only for registers where some lane passes; only a quadrant with a pair
     // past the threshold contributes to dq.
     bool anyp = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) anyp |= s[r] * isk[r] > thq;
+    for (int r = 0; r < 16; ++r) anyp |= s[r] > thq;
     if (__ballot(anyp) != 0ull) {
-      frag kta[NDH * NC];  // K^T by identity, packed as the A operand of the dQ product
-      {
-        f32x16 tr[NDH];
-        transpose_rows<T, DP>(ka, id, tr);
-#pragma unroll
-        for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-          for (int c = 0; c < NC; ++c) kta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-      }
       const int rel0 = i - (k0 + 32 * kh + 8 * half);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float ds = 0.0f;
-        if (__ballot(s[r] * isk[r] > thq) != 0ull) {
+        if (__ballot(s[r] > thq) != 0ull) {
           const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-          const float av = trim(s[r] * isk[r] * iql, hp.r);
+          const float av = trim(s[r] * iql, hp.r);
           if (av > 0.0f && valid && in_window(dd, hp)) {
-            ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r] * isv[r];
+            ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r];
             if (a.drop.on) ds *= dropout_factor(a.drop, bh, i, i - dd);
           }
         }
-        dp[r] = ds * isk[r];
+        dp[r] = ds;
+        __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
       }
-      // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i]
+      // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
+      // the key rows, one 32-column block of d at a time
+      {
+        float sc[16];
+        read_row_scales(sk[w], half, sc);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
+      }
       frag db[NC];
 #pragma unroll
       for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+      for (int dblk = 0; dblk < NDH; ++dblk) {
+        frag f[NC], kt[NC];
 #pragma unroll
-        for (int dblk = 0; dblk < NDH; ++dblk) adq[dblk] = M::mma_ng(kta[dblk * NC + c], db[c], adq[dblk]);
+        for (int c = 0; c < NC; ++c) f[c] = WS::frag(kl, m, dblk * NC + c, half, a.D);
+        f32x16 tr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) tr = M::mma_ng(f[c], ident_frag<T>(c, lane), tr);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kt[c] = M::pack(tr, c * PER);
+        guard_frags(f);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) adq[dblk] = M::mma_ng(kt[c], db[c], adq[dblk]);
+        guard_frags(kt);
+      }
       guard_frags(db);
-      guard_frags(kta);
     }
-    guard_frags(ka);
-    guard_frags(va);
 
-    if (NBUF == 1 && tl[1] >= 0) {
-      wave_lds_sync();  // this wave's reads of the single buffer are done
-      stage_tile(tl[1], 0, mk[1]);
-    }
+    // every LDS read of this tile is done: its buffer takes the next tile
+    wave_lds_sync();
+    if (tl[1] >= 0) stage_tile(tl[1], 0, mk[1]);
     tl[0] = tl[1];
     mk[0] = mk[1];
     tl[1] = walk.next();
   }
   guard_frags(qb);
   guard_frags(hb);
-  guard_frags(id);
 
   // the kh = 1 wave's accumulator reaches the kh = 0 wave through the
   // (now idle) stage buffers
@@ -460,10 +478,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const T* qrow0 = (const T*)a.q + b * a.qs.sb + h * a.qs.sh;
   const T* dh0 = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
   const float* iq0 = a.iqs + (int64_t)bh * a.Tq_pad;
-  const auto plq = S::plan(a.qs.st, a.D, tid), plh = S::plan(DP, DP, tid);
+  // DMA offsets formed at each issue from a laundered thread index (nothing
+  // per-lane kept live across the tile loop)
   auto stage_tile = [&](int qt, int buf) {
-    S::issue(plq, qrow0, a.qs.st, (int64_t)qt * kTile, a.Tq, a.D, stage[buf], tid, w);
-    S::issue(plh, dh0, DP, (int64_t)qt * kTile, a.Tq_pad, DP, stage[buf] + S::TILEB, tid, w);
+    int tx = tid;
+    asm volatile("" : "+v"(tx));
+    const auto plq = S::plan(a.qs.st, a.D, tx), plh = S::plan(DP, DP, tx);
+    S::issue(plq, qrow0, a.qs.st, (int64_t)qt * kTile, a.Tq, a.D, stage[buf], tx, w);
+    S::issue(plh, dh0, DP, (int64_t)qt * kTile, a.Tq_pad, DP, stage[buf] + S::TILEB, tx, w);
     if (w == 0)  // 64 floats of 1/|q|: lanes 0-15 carry them, the rest repeat lane 15 into the slot's tail
       __builtin_amdgcn_global_load_lds(
           (const void __attribute__((address_space(1)))*)(iq0 + (int64_t)qt * kTile + 4 * (lane < 16 ? lane : 15)),

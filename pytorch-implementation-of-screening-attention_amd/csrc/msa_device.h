@@ -457,17 +457,23 @@ struct StageTile {
     col = (((c % CPR) ^ swz(R)) * 16) / (int)sizeof(T);
     if (col >= D) col = 0;
   }
-  // Per-thread element offsets (row R of the tile at R*st) of its chunks.
+  // Per-thread byte offsets (row R of the tile at R*st) of its chunks, as
+  // unsigned 32-bit values: a uniform 64-bit base plus one 32-bit lane offset
+  // is the DMA's scalar-base addressing form.  Valid while a tile spans less
+  // than 2^31 bytes (planned(st)); issue() takes the general path otherwise.
   struct Plan {
-    int off[CPT];
+    uint32_t off[CPT];
   };
+  __device__ static inline bool planned(int64_t st) {
+    return st >= 0 && st * ROWS * (int64_t)sizeof(T) < ((int64_t)1 << 31);
+  }
   __device__ static inline Plan plan(int64_t st, int D, int t) {
     Plan p;
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
       int R, col;
       chunk(u, t, D, R, col);
-      p.off[u] = (int)(R * st) + col;
+      p.off[u] = (uint32_t)((R * st + col) * (int64_t)sizeof(T));
     }
     return p;
   }
@@ -478,12 +484,12 @@ struct StageTile {
   __device__ static inline void issue(const Plan& pl, const T* row0, int64_t st, int64_t r0, int64_t nrows, int D,
                                       char* lds, int t, int grp) {
     const T* base = row0 + r0 * st;
-    if (r0 + ROWS <= nrows) {
+    if (r0 + ROWS <= nrows && planned(st)) {
 #pragma unroll
       for (int u = 0; u < CPT; ++u)
-        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(base + pl.off[u]),
-                                         (void __attribute__((address_space(3)))*)(lds + (u * NT + grp * 64) * 16),
-                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)((const char*)base + (uint64_t)pl.off[u]),
+            (void __attribute__((address_space(3)))*)(lds + (u * NT + grp * 64) * 16), 16, 0, 0);
     } else {
 #pragma unroll
       for (int u = 0; u < CPT; ++u) {
