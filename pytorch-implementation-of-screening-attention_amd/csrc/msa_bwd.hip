@@ -147,10 +147,11 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[DP / 32], const typena
   });
 }
 
-// Waves per SIMD the backward kernels are register-budgeted for: two (256
-// registers a lane) where the bf16 working set fits, else one.
+// Waves per SIMD the backward kernels are register-budgeted for: three (168
+// registers a lane; operands are re-read from LDS rather than held) where the
+// bf16 working set allows, else one.
 template <typename T, int DP>
-constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
+constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 3 : 1; }
 
 // ---------------------------------------------------------------------------
 // dQ (runs first).  256-thread block per 64-query tile of head (b,h); wave w
@@ -164,7 +165,7 @@ constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
 // wave hands its accumulator to the kh = 0 wave through LDS, which finishes dq.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1))) void dq_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   using S = StageTile<T, DP>;
@@ -426,7 +427,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   constexpr int SB = 2 * S::TILEB + 1024;  // per buffer: Q tile | dh tile | 1/|q| (64 floats, 1 KB slot)
   constexpr int KVB = 2 * NKS * kWave * (int)sizeof(frag);  // per key half: own K, V fragments
   // DMA ring of staged query tiles: NBUF buffers, NBUF-1 tiles ahead where LDS allows
-  constexpr int NBUF = 3 * SB + 2 * KVB <= 70 * 1024 ? 3 : (2 * SB + 2 * KVB <= 150 * 1024 ? 2 : 1);
+  // (two buffers for bf16 at D <= 64 keep the block under a third of the LDS,
+  // for three blocks per CU)
+  constexpr int NBUF = bwd_waves<T, DP>() == 3 ? 2
+                       : (3 * SB + 2 * KVB <= 70 * 1024 ? 3 : (2 * SB + 2 * KVB <= 150 * 1024 ? 2 : 1));
   constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile (wave 0 issues one more)
   static_assert(4 * NDH * 16 * kWave * 4 <= NBUF * SB, "exchange must fit the stage buffers");
   __shared__ __attribute__((aligned(16))) char stage[NBUF][SB];
@@ -512,9 +516,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
         kvl[(NKS + ks) * kWave + lane] = kr.v.f[ks];
       }
   }
-  frag id[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
   f32x16 acc_k[NDH], acc_v[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
@@ -538,56 +539,67 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     const int q0 = tl[0] * kTile;
 
     // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
-    // (rows past Tq carry 1/|q| = 0 and dh = 0, so they contribute nothing)
-    frag qa[NKS], ha[NKS];
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      qa[ks] = S::frag(ql, 32 * qh + m, ks, half, a.D);
-      ha[ks] = S::frag(hl, 32 * qh + m, ks, half, DP);
-    }
-    float isq[16];
-    read_row_scales(iql + 32 * qh, half, isq);
-
-    // S = Q K^T and dP = dH V^T (raw operands)
+    // (rows past Tq carry 1/|q| = 0 and dh = 0, so they contribute nothing).
+    // S = Q K^T and dP = dH V^T take one operand pair at a time; the
+    // fragments are re-read from LDS where needed again.
     f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
     {
-      frag kf[NKS], vf[NKS];
+      frag f[NKS], g[NKS];
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        kf[ks] = kvl[ks * kWave + lane];
-        vf[ks] = kvl[(NKS + ks) * kWave + lane];
+        f[ks] = S::frag(ql, 32 * qh + m, ks, half, a.D);
+        g[ks] = kvl[ks * kWave + lane];
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
+      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(f[ks], g[ks], s);
+      guard_frags(f);
+      guard_frags(g);
+    }
+    {
+      frag f[NKS], g[NKS];
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        s = M::mma_ng(qa[ks], kf[ks], s);
-        dp = M::mma_ng(ha[ks], vf[ks], dp);
+        f[ks] = S::frag(hl, 32 * qh + m, ks, half, DP);
+        g[ks] = kvl[(NKS + ks) * kWave + lane];
       }
-      guard_frags(kf);
-      guard_frags(vf);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) dp = M::mma_ng(f[ks], g[ks], dp);
+      guard_frags(f);
+      guard_frags(g);
+    }
+    // register r -> query q0 + 32qh + rowof(r, half), lane -> key j.  Scaled
+    // in place: s = (q . k)/|q|, dp = (dh . v)/|v|.
+    {
+      float sc[16];
+      read_row_scales(iql + 32 * qh, half, sc);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] *= sc[r];
+        dp[r] *= ivl;
+      }
     }
 
-    // register r -> query q0 + 32qh + rowof(r, half), lane -> key j.  A
-    // conservative gate on the raw products (s > thr), then the exact test
+    // A conservative gate on the products (s > thr |k|), then the exact test
     // only for registers where some lane passes; only a quadrant with a pair
     // past the threshold contributes to dk, dv, dr, dw.
     bool anyp = false;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) anyp |= s[r] * isq[r] > thk;
+    for (int r = 0; r < 16; ++r) anyp |= s[r] > thk;
     if (__ballot(anyp) != 0ull) {
       const int rel0 = (q0 + 32 * qh + 8 * half) - j;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float p = 0.0f, ds = 0.0f;
-        if (__ballot(s[r] * isq[r] > thk) != 0ull) {
+        if (__ballot(s[r] > thk) != 0ull) {
           const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-          const float sv = s[r] * isq[r] * ikl;
+          const float sv = s[r] * ikl;
           const float av = trim(sv, hp.r);
           if (av > 0.0f && in_window(dd, hp)) {
             const float c = a.drop.on ? dropout_factor(a.drop, bh, j + dd, j) : 1.0f;
             const float mk = softmask(dd, hp.iw) * c;
-            const float g = dp[r] * ivl;
+            const float g = dp[r];
             p = av * av * mk;
             ds = 2.0f * av * hp.r * mk * g;
             dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
@@ -595,43 +607,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
           }
         }
         s[r] = p;
-        dp[r] = ds * isq[r];
+        dp[r] = ds;
+        __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
+      }
+      {
+        float sc[16];
+        read_row_scales(iql + 32 * qh, half, sc);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp[r] *= sc[r];  // ds/|q|
       }
       // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
-      // with dH^T, Q^T from identity products (packed A operands)
+      // with dH^T, Q^T from identity products on re-read rows, one 32-column
+      // block of d at a time
       frag pb[NC], db[NC];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         pb[c] = M::pack(s, c * PER);
         db[c] = M::pack(dp, c * PER);
       }
-      frag ta[NDH * NC];
-      f32x16 tr[NDH];
-      transpose_rows<T, DP>(ha, id, tr);
 #pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk)
+      for (int dblk = 0; dblk < NDH; ++dblk) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+        for (int op = 0; op < 2; ++op) {  // 0: dH^T P -> dv, 1: Q^T dS -> dk
+          frag f[NC], t[NC];
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+          for (int c = 0; c < NC; ++c)
+            f[c] = op == 0 ? S::frag(hl, 32 * qh + m, dblk * NC + c, half, DP)
+                           : S::frag(ql, 32 * qh + m, dblk * NC + c, half, a.D);
+          f32x16 tr;
 #pragma unroll
-        for (int dblk = 0; dblk < NDH; ++dblk) acc_v[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], acc_v[dblk]);
-      guard_frags(ta);
-      transpose_rows<T, DP>(qa, id, tr);
+          for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk)
+          for (int c = 0; c < NC; ++c) tr = M::mma_ng(f[c], ident_frag<T>(c, lane), tr);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
+          for (int c = 0; c < NC; ++c) t[c] = M::pack(tr, c * PER);
+          guard_frags(f);
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int dblk = 0; dblk < NDH; ++dblk) acc_k[dblk] = M::mma_ng(ta[dblk * NC + c], db[c], acc_k[dblk]);
-      guard_frags(ta);
+          for (int c = 0; c < NC; ++c) {
+            if (op == 0) acc_v[dblk] = M::mma_ng(t[c], pb[c], acc_v[dblk]);
+            else acc_k[dblk] = M::mma_ng(t[c], db[c], acc_k[dblk]);
+          }
+          guard_frags(t);
+        }
+      }
       guard_frags(pb);
       guard_frags(db);
     }
-    guard_frags(qa);
-    guard_frags(ha);
 
     if (NBUF == 1 && tl[1] >= 0) {
       block_sync_lds();  // every wave is done with the single buffer
@@ -642,7 +663,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     tl[2] = NBUF == 3 ? walk.next() : -1;
     if (NBUF < 3) tl[1] = walk.next();
   }
-  guard_frags(id);
 
   // exchange through the (now idle) stage buffers: the qh = 0 wave of each
   // key half finishes dk, the qh = 1 wave dv
