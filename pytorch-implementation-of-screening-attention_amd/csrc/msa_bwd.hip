@@ -441,6 +441,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   const int half = lane >> 5, l32 = lane & 31;
   int kt, bh;
   xcd_interleave(kt, bh);
+  // a key tile's live query tiles lie after it (its window runs forward), so
+  // under a causal mask the lowest key tiles carry the most work: they go first
+  if (a.causal) kt = (int)gridDim.x - 1 - kt;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);

@@ -34,33 +34,44 @@ struct PrepKArgs {
   float eps;
 };
 
-// 16-byte chunk per thread; a key row of DP elements spans CPR threads.
+// 16-byte chunk per thread per row; a key row of DP elements spans CPR
+// threads, and a thread covers kPrepRows rows RPB apart (all loads first).
+constexpr int kPrepRows = 4;
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
   constexpr int VEC = 16 / (int)sizeof(T);
   constexpr int CPR = DP / VEC;  // chunks per row (power of two, <= 32)
   constexpr int RPB = 256 / CPR;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const int64_t t = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;
   const int d0 = (threadIdx.x % CPR) * VEC;
-  const bool valid = t < a.Tk && d0 < a.D;
-  float x[VEC];
-  float ss = 0.0f;
+  float x[kPrepRows][VEC];
 #pragma unroll
-  for (int e = 0; e < VEC; e += 4) {
-    f32x4 v4 = {0.f, 0.f, 0.f, 0.f};
-    if (valid) v4 = load4((const T*)a.k + b * a.ks.sb + t * a.ks.st + h * a.ks.sh + d0 + e);
-    x[e] = v4[0]; x[e + 1] = v4[1]; x[e + 2] = v4[2]; x[e + 3] = v4[3];
-    ss += v4[0] * v4[0] + v4[1] * v4[1] + v4[2] * v4[2] + v4[3] * v4[3];
+  for (int u = 0; u < kPrepRows; ++u) {
+    const int64_t t = ((int64_t)blockIdx.x * kPrepRows + u) * RPB + threadIdx.x / CPR;
+    const bool valid = t < a.Tk && d0 < a.D;
+#pragma unroll
+    for (int e = 0; e < VEC; e += 4) {
+      f32x4 v4 = {0.f, 0.f, 0.f, 0.f};
+      if (valid) v4 = load4((const T*)a.k + b * a.ks.sb + t * a.ks.st + h * a.ks.sh + d0 + e);
+      x[u][e] = v4[0]; x[u][e + 1] = v4[1]; x[u][e + 2] = v4[2]; x[u][e + 3] = v4[3];
+    }
   }
 #pragma unroll
-  for (int o = 1; o < CPR; o <<= 1) ss += __shfl_xor(ss, o);
-  float inv = 1.0f / fmaxf(sqrtf(ss), a.eps);
-  if (t >= a.Tk || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + t])) inv = 0.0f;
-  if (t < a.Tk_pad) {
-    T* p = (T*)a.khat + ((int64_t)bh * a.Tk_pad + t) * DP + d0;
+  for (int u = 0; u < kPrepRows; ++u) {
+    const int64_t t = ((int64_t)blockIdx.x * kPrepRows + u) * RPB + threadIdx.x / CPR;
+    float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < VEC; e += 4) store4(p + e, x[e] * inv, x[e + 1] * inv, x[e + 2] * inv, x[e + 3] * inv);
+    for (int e = 0; e < VEC; ++e) ss += x[u][e] * x[u][e];
+#pragma unroll
+    for (int o = 1; o < CPR; o <<= 1) ss += __shfl_xor(ss, o);
+    float inv = 1.0f / fmaxf(sqrtf(ss), a.eps);
+    if (t >= a.Tk || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + t])) inv = 0.0f;
+    if (t < a.Tk_pad) {
+      T* p = (T*)a.khat + ((int64_t)bh * a.Tk_pad + t) * DP + d0;
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4)
+        store4(p + e, x[u][e] * inv, x[u][e + 1] * inv, x[u][e + 2] * inv, x[u][e + 3] * inv);
+    }
   }
   // clear this head's live-tile bitmap rows; the screen ORs live bits in
   uint32_t* brow = a.bits + (int64_t)bh * a.bits_per_bh;
@@ -610,7 +621,7 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
     pa.k = c.k; pa.ks = c.ks; pa.kpm = c.kpm; pa.khat = c.khat;
     pa.bits = c.bits; pa.bits_per_bh = (int64_t)g.nqt * g.nkt_words;
     pa.H = g.H; pa.Tk = g.Tk; pa.D = g.D; pa.Tk_pad = g.Tk_pad; pa.eps = c.eps;
-    constexpr int RPB = 256 / (DP * (int)sizeof(T) / 16);
+    constexpr int RPB = 256 / (DP * (int)sizeof(T) / 16) * kPrepRows;
     timer_begin(1, c.stream);
     hipLaunchKernelGGL((prep_k_kernel<T, DP>), dim3((unsigned)((g.Tk_pad + RPB - 1) / RPB), (unsigned)(g.B * g.H)),
                        dim3(256), 0, c.stream, pa);
