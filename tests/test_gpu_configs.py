@@ -1,0 +1,166 @@
+"""GPU checks at the full shapes of the benchmark configurations other than the
+headline one (which test_gpu_parity covers):
+
+  * long-context prefill, B=1, T=100,000, H=8, D=64, bf16, causal, r=2,
+    w log-uniform in [512, 1e5]: sampled output rows against the float64
+    oracle, with planted long-range matches inside and outside the windows;
+  * one MultiscreenLM training step (vocab 50257, d_model 512, 8 heads,
+    6 layers, T=2048, Zipf(1.1) ids): logits, loss and every parameter
+    gradient against the same model whose attention core is the explicit
+    T x T matrix form (_dense.py) evaluated in float32;
+  * KV-cache decode, batch 16 against a 100,000-position bf16 cache through
+    the 6-layer LM: 256 greedy steps, each step's logits against a full
+    forward() over the finished sequence.
+
+Tolerances are the north star's (max|got-ref|/max|ref| per tensor): 1e-5 in
+fp32 and 2e-2 in bf16.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import screening_oracle as O
+from helpers import np64, rel_err
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+VOCAB = 50257
+
+
+def _ops():
+    from multiscreen import ops
+    return ops
+
+
+def _t_rel(got, ref):
+    """rel_err on device tensors (max|got-ref| / max|ref|), in float64."""
+    got, ref = got.double(), ref.double()
+    scale = ref.abs().max().item()
+    diff = (got - ref).abs().max().item()
+    return diff / scale if scale else diff
+
+
+def test_cfg4_long_prefill_sampled_rows_bf16():
+    B, T, H, D = 1, 100000, 8, 64
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(B, T, H, D, generator=g).bfloat16() for _ in range(3))
+    r = [2.0] * H
+    lo, hi = math.log(512.0), math.log(1e5)
+    w = torch.exp(lo + (hi - lo) * torch.rand(H, generator=g)).tolist()
+    # row -> distance of a planted key equal to that row's query: inside some
+    # heads' windows (live pair far back), or beyond every window (must vanish)
+    plants = {4095: 3000, 50000: 40000, 70001: 12000, 99935: 99000, 99999: 20000}
+    for i, d in plants.items():
+        k[0, i - d] = q[0, i]
+    assert max(w) < 99000
+    rows = [0, 1, 63, 64, 127, 4095, 4096, 30000, 50000, 70001, 99935, 99967, 99968, 99999]
+    ops = _ops()
+    rg = torch.tensor(r, device=DEV)
+    wg = torch.tensor(w, device=DEV)
+    y = ops.fwd_raw(q.to(DEV), k.to(DEV), v.to(DEV), rg, wg, True, 1e-8, None)[0]
+    torch.cuda.synchronize()
+    yref = O.rows_forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), rows, True)
+    got = np64(y[:, rows])
+    # the planted in-window pairs carry most of the sampled output
+    assert np.max(np.abs(yref[:, rows.index(4095)])) > 0.1
+    assert np.max(np.abs(yref[:, rows.index(99999)])) > 0.05
+    assert rel_err(got, yref) <= 2e-2
+    # a row whose planted match lies beyond every window keeps only its few
+    # natural near-threshold pairs (oracle max ~2e-5 here)
+    assert np.max(np.abs(got[:, rows.index(99935)])) < 1e-3
+
+
+def _zipf_ids(B, T, s, seed):
+    g = torch.Generator().manual_seed(seed)
+    p = torch.arange(1, VOCAB + 1, dtype=torch.float64).pow(-s)
+    ids = torch.multinomial((p / p.sum()).float(), B * T, replacement=True, generator=g)
+    return ids.view(B, T)
+
+
+def _dense_core(attn):
+    """attn.core with the explicit-matrix form, computed in float32."""
+    from multiscreen._dense import screening_core_dense
+
+    def core(q, k, v, key_padding_mask=None):
+        y = screening_core_dense(q.float(), k.float(), v.float(), attn.sharpness().float(),
+                                 attn.window().float(), attn.causal, attn.eps, key_padding_mask)
+        return y.to(q.dtype)
+    return core
+
+
+def _lm(max_seq_len, dtype, seed=0, s_r=None, s_v=None):
+    from multiscreen import MultiscreenLM
+    torch.manual_seed(seed)
+    lm = MultiscreenLM(vocab_size=VOCAB, d_model=512, num_heads=8, num_layers=6,
+                       max_seq_len=max_seq_len)
+    with torch.no_grad():
+        for blk in lm.blocks:
+            if s_r is not None:
+                blk.attn.s_r.copy_(torch.as_tensor(s_r, dtype=torch.float32))
+            if s_v is not None:
+                blk.attn.s_v.copy_(torch.as_tensor(s_v, dtype=torch.float32))
+    return lm.to(DEV, dtype)
+
+
+def _train_step(lm, ids):
+    lm.zero_grad(set_to_none=True)
+    out = lm(ids, labels=ids)
+    out["loss"].backward()
+    torch.cuda.synchronize()
+    grads = {n: p.grad.detach().clone() for n, p in lm.named_parameters()}
+    return out["loss"].detach(), out["logits"].detach(), grads
+
+
+@pytest.mark.parametrize("dtype,B", [(torch.float32, 2), (torch.bfloat16, 8)], ids=["f32", "bf16"])
+def test_cfg3_lm_training_step_matches_dense_core(dtype, B):
+    # at init the q/k projections are independent, so r must sit well below 2
+    # for the sims (std 1/8) to pass the threshold at all; windows span 2..2048
+    s_r = [math.log(0.15)] * 8
+    s_v = torch.linspace(0.0, math.log(2047.0), 8)
+    lm = _lm(2048, dtype, s_r=s_r, s_v=s_v)
+    ids = _zipf_ids(B, 2048, 1.1, seed=3).to(DEV)
+    loss, logits, grads = _train_step(lm, ids)
+    assert math.isfinite(loss.item())
+    for blk in lm.blocks:
+        blk.attn.core = _dense_core(blk.attn)
+    loss_r, logits_r, grads_r = _train_step(lm, ids)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert abs(loss.item() - loss_r.item()) <= tol * abs(loss_r.item())
+    assert _t_rel(logits, logits_r) <= tol
+    for name, gr in grads_r.items():
+        assert gr.abs().max().item() > 0, name
+        assert _t_rel(grads[name], gr) <= tol, name
+
+
+def test_cfg5_decode_100k_cache_matches_full_forward():
+    B, CAP, STEPS = 16, 100000, 256
+    # every layer: windows 16 .. 1e5 (one head reads the whole cache), r = 1.3
+    s_r = [math.log(0.3)] * 8
+    s_v = torch.log(torch.logspace(math.log10(16.0), 5.0, 8) - 1.0)
+    lm = _lm(CAP, torch.bfloat16, s_r=s_r, s_v=s_v).eval()
+    g = torch.Generator().manual_seed(5)
+    prompt = torch.randint(0, VOCAB, (B, CAP - STEPS), generator=g).to(DEV)
+    caches = lm.new_cache(B, CAP, torch.bfloat16, DEV)
+    with torch.no_grad():
+        logits = lm.prefill(prompt, caches)
+        steps, toks = [logits.float()], []
+        for s in range(STEPS):
+            tok = logits.argmax(-1, keepdim=True)
+            toks.append(tok)
+            if s + 1 < STEPS:
+                logits = lm.decode_step(tok, caches, CAP - STEPS + s)
+                steps.append(logits.float())
+        seq = torch.cat([prompt] + toks, dim=1)
+        assert seq.shape == (B, CAP)
+        x = lm.embed(seq)
+        for blk in lm.blocks:
+            x = blk(x)
+        ref = lm._head(x[:, CAP - STEPS - 1:CAP - 1]).float()
+    torch.cuda.synchronize()
+    got = torch.stack(steps, dim=1)
+    assert got.shape == ref.shape
+    assert _t_rel(got, ref) <= 2e-2
