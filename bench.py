@@ -61,13 +61,18 @@ def window_tiles(T, w_list, tile=64):
     return n
 
 
-def popcount_bits(bits):
+def live_counts(bits, B, H, T):
+    """(live 32x32 units, live 64x64 tiles) from the live-unit bitmap: per
+    (b, h), 2*nqt rows of ceil(2*nkt/32) words; a tile is live iff one of its
+    four units is."""
     import torch
-    b = bits.to(torch.int64) & 0xFFFFFFFF
-    c = torch.zeros_like(b)
-    for s in range(32):
-        c += (b >> s) & 1
-    return int(c.sum())
+    nqt = nkt = (T + 63) // 64
+    words = (2 * nkt + 31) // 32
+    b = (bits.to(torch.int64) & 0xFFFFFFFF)[:B * H * 2 * nqt * words].view(B * H, 2 * nqt, words, 1)
+    sh = torch.arange(32, device=bits.device, dtype=torch.int64)
+    u = ((b >> sh) & 1).view(B * H, 2 * nqt, words * 32)[:, :, :2 * nkt].bool()
+    tiles = u.view(B * H, nqt, 2, nkt, 2).any(dim=4).any(dim=2)
+    return int(u.sum()), int(tiles.sum())
 
 
 def kernel_times(L, kid, fn, n):
@@ -230,11 +235,13 @@ def main():
     dom_ms = sum(buf[i] for i in range(n)) / max(1, n)
 
     nW = window_tiles(T, w) * B
-    nA = popcount_bits(bits)
-    f_total = TILE_FLOP * (nW + 6 * nA)
-    # algorithmic flop of each kernel: the screen Q K^T over W; alpha V over A;
-    # the backward's S recompute, dP, dV, dK in dkdv and dQ in dq over A
-    alg_flop = {"fwd_screen_kernel": TILE_FLOP * nW, "fwd_live_kernel": TILE_FLOP * nA,
+    nU, nA = live_counts(bits, B, H, T)
+    UNIT_FLOP = TILE_FLOP // 4  # one 32x32 unit product with D=64
+    f_total = TILE_FLOP * nW + UNIT_FLOP * nU + 5 * TILE_FLOP * nA
+    # algorithmic flop of each kernel: the screen Q K^T over W (64x64 tiles);
+    # alpha V over the live 32x32 units U; the backward's S recompute, dP, dV,
+    # dK in dkdv and dQ in dq over the live 64x64 tiles A
+    alg_flop = {"fwd_screen_kernel": TILE_FLOP * nW, "fwd_live_kernel": UNIT_FLOP * nU,
                 "dkdv_kernel": TILE_FLOP * 4 * nA, "dq_kernel": TILE_FLOP * nA}
     dom_flop = alg_flop.get(dom)
     achieved = dom_flop / (dom_ms * 1e-3) / 1e12 if dom_flop else None
@@ -265,6 +272,7 @@ def main():
                      "traffic_source": "profiles/fwd_bwd_cfg2_pmc_bytes.txt",
                      "flop_per_launch": dom_flop},
         "tiles": {"causal": B * H * (T // 64) * (T // 64 + 1) // 2, "window": nW, "active": nA,
+                  "active_units_32": nU,
                   "window_skip": round(1 - nW / (B * H * (T // 64) * (T // 64 + 1) / 2), 4),
                   "threshold_skip": round(1 - nA / nW, 5)},
         "step_tflops_alg": round(step_tflops, 2),

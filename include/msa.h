@@ -77,10 +77,11 @@ const char* msa_last_error(void);
  * 32/64/128) that the forward stages through LDS.  Not needed afterwards. */
 size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
-/* Number of uint32 words of the active-tile bitmap: one bit per
- * (b, h, 64-query tile, 64-key tile), set iff some in-window, unmasked pair of
- * the tile has alpha > 0.  Row (b, h, query tile) holds ceil(nkt/32) words,
- * bit kt%32 of word kt/32. */
+/* Number of uint32 words of the live-unit bitmap: one bit per
+ * (b, h, 32-query unit, 32-key unit), set iff some in-window, unmasked pair of
+ * the unit has alpha > 0.  With nqt = ceil(Tq/64), nkt = ceil(Tk/64), the
+ * (b, h) block holds 2*nqt rows (query unit qu: queries 32qu .. 32qu+31) of
+ * ceil(2*nkt/32) words; key unit ku is bit ku%32 of word ku/32 of the row. */
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);
 
 /* Bytes of backward workspace: one (dr, dw) partial per (b, h, 64-key tile),

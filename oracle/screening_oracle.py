@@ -317,9 +317,9 @@ def decode_row(q_new, kcache, vcache, cache_len, r, w, eps=EPS):
 
 
 def tile_counts(q, k, r, w, causal=True, eps=EPS, tile=64, key_padding_mask=None, block=512):
-    """(|W|, |A|, active) over all heads: W = 64x64 tiles holding an in-window
-    pair; A = tiles holding an in-window, unmasked pair with 1 - r(1-s) > 0.
-    `active` is the (B,H,nqt,nkt) bool map of A."""
+    """(|W|, |A|, active) over all heads: W = tile x tile blocks (64 or 32)
+    holding an in-window pair; A = blocks holding an in-window, unmasked pair
+    with 1 - r(1-s) > 0.  `active` is the (B,H,nqt,nkt) bool map of A."""
     qn, kn = normalize(_heads(q), eps), normalize(_heads(k), eps)
     B, H, Tq, D = qn.shape
     Tk = kn.shape[2]

@@ -63,7 +63,7 @@ struct BwdKArgs {
   const uint32_t* bits;
   void* dq; void* dk; void* dv; float* part;
   void* dh; float* iqs;  // workspace: dh [b*h][Tq_pad][DP] (T), 1/|q| [b*h][Tq_pad]
-  int B, H, Tq, Tk, D, nqt, nkt, nkt_words, causal;
+  int B, H, Tq, Tk, D, nqt, nkt, nku_words, causal;
   int64_t Tq_pad;
   float eps;
   Dropout drop;
@@ -199,8 +199,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   if (jlo < 0) jlo = 0;
   if (jhi > a.Tk - 1) jhi = a.Tk - 1;
   const int kt_lo = (int)(jlo / kTile), kt_hi = jhi >= jlo ? (int)(jhi / kTile) : kt_lo - 1;
-  const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
-  auto bitf = [brow](int kl) { return ((brow[kl >> 5] >> (kl & 31)) & 1u) != 0u; };
+  // key tile kl is live for this query tile iff one of its four 32x32 units
+  // is: bits 2kl, 2kl+1 of the rows of query units 2qt, 2qt+1
+  const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + 2 * qt) * a.nku_words;
+  const int nw = a.nku_words;
+  auto bitf = [brow, nw](int kl) { return (((brow[kl >> 4] | brow[nw + (kl >> 4)]) >> ((2 * kl) & 31)) & 3u) != 0u; };
   BitWalk<decltype(bitf)> walk(bitf, kt_lo, kt_hi);
   int cur = walk.next();
   if (cur < 0) {  // block-uniform: no live key tile, dq = 0
@@ -459,9 +462,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
   if (ilo < 0) ilo = 0;
   if (ihi > a.Tq - 1) ihi = a.Tq - 1;
   const int qt_lo = (int)(ilo / kTile), qt_hi = ihi >= ilo ? (int)(ihi / kTile) : qt_lo - 1;
-  const uint32_t* bcol = a.bits + (int64_t)bh * a.nqt * a.nkt_words + (kt >> 5);
-  const int nw = a.nkt_words, sh = kt & 31;
-  auto bitf = [bcol, nw, sh](int ql) { return ((bcol[(int64_t)ql * nw] >> sh) & 1u) != 0u; };
+  // query tile ql is live for this key tile iff one of its four 32x32 units
+  // is: bits 2kt, 2kt+1 of the rows of query units 2ql, 2ql+1
+  const uint32_t* bcol = a.bits + (int64_t)bh * 2 * a.nqt * a.nku_words + (kt >> 4);
+  const int nw = a.nku_words, sh = (2 * kt) & 31;
+  auto bitf = [bcol, nw, sh](int ql) {
+    return (((bcol[(int64_t)2 * ql * nw] | bcol[(int64_t)(2 * ql + 1) * nw]) >> sh) & 3u) != 0u;
+  };
   BitWalk<decltype(bitf)> walk(bitf, qt_lo, qt_hi);
   int cur = walk.next();
   if (cur < 0) {  // block-uniform: no live query tile, dk = dv = 0
@@ -749,7 +756,7 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   ka.dh = ws + bwd_part_bytes(g);
   ka.iqs = (float*)(ws + bwd_part_bytes(g) + bwd_dh_bytes(g));
   ka.B = g.B; ka.H = g.H; ka.Tq = g.Tq; ka.Tk = g.Tk; ka.D = g.D;
-  ka.nqt = g.nqt; ka.nkt = g.nkt; ka.nkt_words = g.nkt_words; ka.causal = g.causal;
+  ka.nqt = g.nqt; ka.nkt = g.nkt; ka.nku_words = g.nku_words; ka.causal = g.causal;
   ka.Tq_pad = g.Tq_pad;
   ka.eps = c.eps;
   ka.drop = c.drop;

@@ -34,7 +34,7 @@ int ok() {
   return MSA_OK;
 }
 
-constexpr int kMaxT = 1 << 22;  // tile bitmap rows are kept to <= 2048 words
+constexpr int kMaxT = 1 << 22;  // live-unit bitmap rows are kept to <= 4096 words
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -49,7 +49,7 @@ int check_geometry(int B, int H, int Tq, int Tk, int D, int dtype, int causal, m
   g->B = B; g->H = H; g->Tq = Tq; g->Tk = Tk; g->D = D; g->DP = msa::padded_dim(D);
   g->dtype = dtype; g->causal = causal ? 1 : 0;
   g->nqt = msa::ntiles(Tq); g->nkt = msa::ntiles(Tk);
-  g->nkt_words = (g->nkt + 31) / 32;
+  g->nku_words = (2 * g->nkt + 31) / 32;
   g->Tq_pad = (int64_t)g->nqt * 64; g->Tk_pad = (int64_t)g->nkt * 64;
   g->esize = dtype == MSA_BF16 ? 2 : 4;
   return MSA_OK;
@@ -62,6 +62,12 @@ int check_tensor(const char* name, const void* p, int64_t sb, int64_t st, int64_
   if (sb < 0 || st < 0 || sh < 0 || sb % m || st % m || sh % m)
     return fail(MSA_ERR_INVALID, "%s strides (%lld,%lld,%lld) must be non-negative multiples of %lld elements", name,
                 (long long)sb, (long long)st, (long long)sh, (long long)m);
+  // kernels address the rows of a 64-row tile by 32-bit byte offsets from the
+  // tile's first row
+  const int64_t es = dtype == MSA_BF16 ? 2 : 4;
+  if (st * 64 * es >= (int64_t)1 << 32)
+    return fail(MSA_ERR_INVALID, "%s time stride %lld elements is too large (64 rows must span < 4 GiB)", name,
+                (long long)st);
   return MSA_OK;
 }
 
@@ -170,7 +176,7 @@ size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype) {
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk) {
   if (B < 0 || H <= 0 || Tq < 0 || Tk < 0) return 0;
   const int64_t nqt = msa::ntiles(Tq), nkt = msa::ntiles(Tk);
-  return (size_t)((int64_t)B * H * nqt * ((nkt + 31) / 32));
+  return (size_t)((int64_t)B * H * 2 * nqt * ((2 * nkt + 31) / 32));
 }
 
 size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype) {

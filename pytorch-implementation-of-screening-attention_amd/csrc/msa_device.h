@@ -16,6 +16,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
 constexpr int kWave = 64;
 constexpr int kTile = 64;  // rows of a query tile and of a key tile
+constexpr int kUnit = 32;  // rows of a query unit and of a key unit (live-unit bitmap)
 
 // ---------------------------------------------------------------------------
 // MFMA fragments.  Both element types use the 32x32 output block; a wave-64

@@ -86,21 +86,26 @@ struct FwdKArgs {
   const float* r; const float* w;
   void* y; float* hnorm; uint32_t* bits;
   Dropout drop;
-  int H, Tq, Tk, D, nqt, nkt_words, causal;
+  int H, Tq, Tk, D, nqt, nku_words, causal;
   int nsegl;  // screen blocks per 4-query-tile group (segment stride)
   int64_t Tk_pad;
   float eps;
 };
 
-// Key-tile range [lo, hi] of the window of queries [qa, qb].
-__device__ inline void key_tile_range(const FwdKArgs& a, const HeadParams& hp, bool causal, int64_t qa, int64_t qb,
-                                      int& lo, int& hi) {
+// Range [lo, hi] of the U-key blocks that hold the window of queries [qa, qb].
+template <int U>
+__device__ inline void key_range(const FwdKArgs& a, const HeadParams& hp, bool causal, int64_t qa, int64_t qb,
+                                 int& lo, int& hi) {
   int64_t jlo = qa - hp.wc + 1;
   int64_t jhi = causal ? qb : qb + hp.wc - 1;
   if (jlo < 0) jlo = 0;
   if (jhi > a.Tk - 1) jhi = a.Tk - 1;
-  lo = (int)(jlo / kTile);
-  hi = jhi >= jlo ? (int)(jhi / kTile) : lo - 1;
+  lo = (int)(jlo / U);
+  hi = jhi >= jlo ? (int)(jhi / U) : lo - 1;
+}
+__device__ inline void key_tile_range(const FwdKArgs& a, const HeadParams& hp, bool causal, int64_t qa, int64_t qb,
+                                      int& lo, int& hi) {
+  key_range<kTile>(a, hp, causal, qa, qb, lo, hi);
 }
 
 template <typename T, int DP>
@@ -200,7 +205,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   }
   frag qf[2 * NKS];
   float iq[2];
-  uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + (wave_ok ? qt : 0)) * a.nkt_words;
+  // bitmap rows of the wave's two query units (32 queries each)
+  uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + 2 * (wave_ok ? qt : 0)) * a.nku_words;
 
   // DMA: chunk c = u*256 + tid of a tile (row c / CPR, LDS position c % CPR)
   // comes from global chunk position ^ swz(row) of that row; the per-lane
@@ -258,12 +264,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   };
   // Threshold vote on key half kh of the tile at k0, per lane (no ballot): a(s)
-  // is monotone in s and s = acc/|q_i|, so the half has a live pair iff its
-  // largest in-window acc passes.  Register r of the half holds key
+  // is monotone in s and s = acc/|q_i|, so a 32x32 unit has a live pair iff
+  // its largest in-window acc passes.  Register r of the half holds key
   // k0 + 32kh + 16(r/8) + 8half + r%8.  Tiles wholly inside every pair's
-  // window skip the per-register window test.
-  auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh, bool interior) -> bool {
-    bool lv = false;
+  // window skip the per-register window test.  Bit qh of the result: this
+  // lane's query of unit qh passes.
+  auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh, bool interior) -> int {
+    int lv = 0;
 #pragma unroll
     for (int qh = 0; qh < 2; ++qh) {
       float mx = -INFINITY;
@@ -276,7 +283,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         for (int r = 0; r < 16; ++r)
           mx = fmaxf(mx, in_window(rel0 - (16 * (r >> 3) + (r & 7)), hp) ? acc[qh][r] : -INFINITY);
       }
-      lv |= trim(mx * iq[qh], hp.r) > 0.0f;
+      lv |= (trim(mx * iq[qh], hp.r) > 0.0f ? 1 : 0) << qh;
     }
     return lv;
   };
@@ -286,11 +293,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int d_max = q0 + 63 - kt * kTile, d_min = q0 - kt * kTile - 63;
     return in_window(d_max, hp) && in_window(d_min, hp);
   };
-  // Live tiles are rare (a few percent of the window): one lane ORs the bit of
-  // each into the bitmap (cleared by prep_k_kernel), so segments that share a
-  // bitmap word need no ordering.
-  auto finish = [&](int kd, bool lv) {
-    if (__ballot(lv) != 0 && wave_ok && lane == 0) atomicOr(&brow[kd >> 5], 1u << (kd & 31));
+  // Live tiles are rare (a few percent of the window): one lane ORs the bits
+  // of tile kd's live units into the bitmap (cleared by prep_k_kernel), so
+  // segments that share a bitmap word need no ordering.  v0, v1: the votes
+  // of key halves 0 and 1 (bit qh per lane).
+  auto finish = [&](int kd, int v0, int v1) {
+    const int vv = v0 | (v1 << 2);
+    if (__ballot(vv != 0) != 0 && wave_ok) {
+      // row qh, key units 2kd (bit 0) and 2kd + 1 (bit 1): one word
+      const uint32_t m0 = (__ballot(vv & 1) != 0 ? 1u : 0u) | (__ballot(vv & 4) != 0 ? 2u : 0u);
+      const uint32_t m1 = (__ballot(vv & 2) != 0 ? 1u : 0u) | (__ballot(vv & 8) != 0 ? 2u : 0u);
+      const int u = 2 * kd;
+      if (lane == 0 && m0 != 0u) atomicOr(&brow[u >> 5], m0 << (u & 31));
+      if (lane == 0 && m1 != 0u) atomicOr(&brow[a.nku_words + (u >> 5)], m1 << (u & 31));
+    }
   };
 
   // Tiles past a segment's last tile shi are replaced by shi itself: the ring
@@ -321,7 +337,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     // 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).  Tile kt sits
     // in ring slot (kt - slo) % NST.
     f32x16 acc0[2], acc1[2];
-    bool pend = false, live0 = false, pint = false;  // tile kt-1: keys 32-63 pending in acc1
+    bool pend = false, pint = false;  // tile kt-1: keys 32-63 pending in acc1
+    int live0 = 0;                    // tile kt-1: vote on keys 0-31
     int pk0 = 0;
     auto enter = [&](int kt) -> const char* {
       // tile kt's DMA (own part) is complete once only the two younger tiles'
@@ -337,7 +354,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       const char* slot = enter(kt);
       const bool mine = kt >= kt_lo && kt <= kt_hi;
       if (mine) half_mma(slot, 0, acc0);
-      if (kt > slo) finish(kt - 1, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
+      if (kt > slo && pend) finish(kt - 1, live0, vote_half(acc1, pk0, 1, pint));
       if (mine) {
         half_mma(slot, 1, acc1);
         pint = interior_tile(kt);
@@ -353,7 +370,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     auto step_inside = [&](int kt) {
       const char* slot = enter(kt);
       half_mma(slot, 0, acc0);
-      finish(kt - 1, pend & (live0 | vote_half(acc1, 0, 1, true)));
+      finish(kt - 1, pend ? live0 : 0, pend ? vote_half(acc1, 0, 1, true) : 0);
       half_mma(slot, 1, acc1);
       live0 = vote_half(acc0, 0, 0, true);
       pend = true;
@@ -378,7 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       for (; kt <= ib; ++kt) step_inside(kt);
     }
     for (; kt <= shi; ++kt) step(kt);
-    finish(shi, pend && (live0 || vote_half(acc1, pk0, 1, pint)));
+    if (pend) finish(shi, live0, vote_half(acc1, pk0, 1, pint));
     // the replacement loads are done and every wave is done with the ring
     // before the next segment refills it
     wait_vmcnt<0>();
@@ -388,53 +405,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 }
 
 // ---------------------------------------------------------------------------
-// Live tiles.  256-thread block per 64-query tile; wave w works on the
-// quadrant (queries 32*qh .. +31, keys 32*kh .. +31) of every key tile the
-// screen marked live, qh = w/2, kh = w%2.  Lane -> query i = q0 + 32*qh + l32,
-// registers -> keys.  The live key tiles' K^ rows (workspace) and raw V rows
-// are staged into LDS by DMA, double-buffered: tile n+1 streams in while tile
-// n is computed.  Per tile: S^T from K^ (the screen's operands and order, so
-// the same values), alpha*m (attention.py:92-119) with 1/|v_j| folded in, and
-// H^T += V^T P^T with V^T from an identity MFMA on the raw V rows.  The kh = 1
-// wave hands its H^T to the kh = 0 wave through LDS, which applies TanhNorm
-// (norm.py:23-25) and writes y in (B,T,H,D) and |h| per row.  Rows with no
-// live tile get y = 0, |h| = 0.
+// Live units.  One wave (a 64-thread block) per query unit: 32 consecutive
+// queries of one head, lane -> query i = 32*qu + l%32.  The wave walks its
+// row of the live-unit bitmap; for each live key unit (32 keys) it loads the
+// K^ rows (workspace) and raw V rows straight from global memory as MFMA
+// operands, the next unit's loads in flight while the current one is
+// computed: S^T from K^ (the screen's operands and order, so the same
+// values), alpha*m (attention.py:92-119) with 1/|v_j| folded in, and
+// H^T += V^T P^T with V^T from an identity MFMA on the raw V rows.  The
+// epilogue applies TanhNorm (norm.py:23-25) and writes y in (B,T,H,D) and |h|
+// per row.  Units with no live key unit get y = 0, |h| = 0.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1)))
 void fwd_live_kernel(FwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
-  using S = StageTile<T, DP>;
+  using R = PRow<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  // DMA ring of staged key tiles: NBUF buffers, NBUF-1 tiles ahead
-  constexpr int NBUF = 3 * 2 * S::TILEB <= 100 * 1024 ? 3 : 2;
-  constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile
-  __shared__ __attribute__((aligned(16))) char stage[NBUF][2 * S::TILEB];  // [buffer][K^ tile | V tile]
-  __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v_j| of its key rows
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
-  const int half = lane >> 5, l32 = lane & 31;
-  int qt, bh;
-  xcd_interleave(qt, bh);
+  __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  int qu, bh;
+  xcd_interleave(qu, bh);
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);
-  const int q0 = qt * kTile;
-  const int i = q0 + 32 * qh + l32;
+  const int i = qu * kUnit + l32;
   const bool valid = i < a.Tq;
   // output row of query i (formed where it is stored, so nothing holds it
-  // across the tile loop)
+  // across the unit loop)
   auto yrow = [&]() { return (T*)a.y + (((int64_t)b * a.Tq + (valid ? i : 0)) * a.H + h) * a.D; };
 
-  int kt_lo, kt_hi;
-  key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
-  const uint32_t* brow = a.bits + ((int64_t)bh * a.nqt + qt) * a.nkt_words;
-  auto bitf = [brow](int kl) { return ((brow[kl >> 5] >> (kl & 31)) & 1u) != 0u; };
-  BitWalk<decltype(bitf)> walk(bitf, kt_lo, kt_hi);
+  int ku_lo, ku_hi;
+  {
+    const int qa = qu * kUnit, qb = qa + kUnit - 1 < a.Tq - 1 ? qa + kUnit - 1 : a.Tq - 1;
+    key_range<kUnit>(a, hp, causal, qa, qb, ku_lo, ku_hi);
+  }
+  const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + qu) * a.nku_words;
+  auto bitf = [brow](int u) { return ((brow[u >> 5] >> (u & 31)) & 1u) != 0u; };
+  BitWalk<decltype(bitf)> walk(bitf, ku_lo, ku_hi);
   int cur = walk.next();
-  if (cur < 0) {  // block-uniform: no live key tile, y = 0 and |h| = 0
-    if (kh == 0 && valid) {
+  if (cur < 0) {  // wave-uniform: no live key unit, y = 0 and |h| = 0
+    if (valid) {
       if (half == 0) a.hnorm[(int64_t)bh * a.Tq + i] = 0.0f;
 #pragma unroll
       for (int dblk = 0; dblk < NDH; ++dblk)
@@ -447,151 +459,143 @@ void fwd_live_kernel(FwdKArgs a) {
     return;
   }
 
+  // key row of this lane in unit u: 32u + perm_row(l32) (A-operand order)
+  const int m = perm_row(l32);
   const T* kg = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
-  const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
-  const auto plk = S::plan(DP, DP, tid), plv = S::plan(a.vs.st, a.D, tid);
-  auto stage_tile = [&](int kt, int buf) {
-    S::issue(plk, kg, DP, (int64_t)kt * kTile, a.Tk_pad, DP, stage[buf], tid, w);
-    S::issue(plv, vrow0, a.vs.st, (int64_t)kt * kTile, a.Tk, a.D, stage[buf] + S::TILEB, tid, w);
+  const T* vg = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
+  // The lane's chunks (elements KS*ks + PER*half) of its row of key unit u,
+  // from one row address and immediate offsets.  K^ rows exist up to Tk_pad
+  // (zero past Tk and for masked keys, so those keys never pass the
+  // threshold and their P is exactly 0); V rows past Tk read row Tk-1
+  // instead, which P = 0 then cancels.  Only D = 16 < DP has chunks past D,
+  // and they hold zeros.
+  // Addresses: a wave-uniform 64-bit unit base plus a 32-bit lane offset.
+  const uint32_t koff = (uint32_t)((m * DP + PER * half) * (int)sizeof(T));
+  auto load_k = [&](int u, frag (&f)[NKS]) {
+    const char* p = (const char*)(kg + (int64_t)u * kUnit * DP) + koff;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) f[ks] = M::load((const T*)(p + KS * ks * (int)sizeof(T)));
+  };
+  auto load_v = [&](int u, frag (&f)[NKS]) {
+    const int r = u * kUnit + m < a.Tk ? m : a.Tk - 1 - u * kUnit;
+    const uint32_t off = (uint32_t)(((int64_t)r * a.vs.st + PER * half) * (int64_t)sizeof(T));
+    const char* p = (const char*)(vg + (int64_t)u * kUnit * a.vs.st) + off;
+    // chunks past D (D = 16 < DP = 32 only) re-read chunk 0; vzero clears them
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int c = DP == 32 && KS * ks >= a.D ? 0 : KS * ks;
+      f[ks] = M::load((const T*)(p + c * (int)sizeof(T)));
+    }
+  };
+  auto vzero = [&](frag (&f)[NKS]) {
+    if constexpr (DP == 32) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        if (KS * ks >= a.D) f[ks] = M::zero();
+    }
   };
   // own queries as raw B operands (lane -> query) and 1/|q_i|; their loads go
-  // first, the first key tiles' DMA behind them (vector memory returns in order)
-  // tl[n]: the n-th next live key tile (-1 past the end)
-  int tl[3] = {cur, -1, -1};
+  // first, the first unit's behind them
   frag qf[NKS];
   float iq;
+  frag kc[NKS], vc[NKS];
   {
-    PRow<T, DP> qr;
+    R qr;
     qr.load((const T*)a.q + b * a.qs.sb + (int64_t)(valid ? i : 0) * a.qs.st + h * a.qs.sh, valid, a.D, half);
-    stage_tile(tl[0], 0);
-    for (int n = 1; n < NBUF; ++n) tl[n] = walk.next();
-    if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
+    load_k(cur, kc);
+    load_v(cur, vc);
     iq = qr.inv_norm(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
   }
   const float thq = hp.thr / iq;  // s > thr  <=>  k^ . q > thr |q|
-  frag id[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
   f32x16 o[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dblk][r] = 0.0f;
-  const int m = perm_row(l32);
 
-  for (int it = 0; tl[0] >= 0; ++it) {
-    // tile tl[0] is in LDS once this wave's older DMA is done and every wave
-    // passed the barrier; the buffer refilled next was read last iteration
-    if (NBUF == 3 && tl[1] >= 0) wait_vmcnt<PT>();
-    else wait_vmcnt<0>();
-    block_sync_lds();
-    if (tl[NBUF - 1] >= 0) stage_tile(tl[NBUF - 1], (it + NBUF - 1) % NBUF);
-    const char* kl = stage[it % NBUF];
-    const char* vl = kl + S::TILEB;
-    const int k0 = tl[0] * kTile;
-
-    // key rows j = k0 + 32*kh + perm_row(l32): K^ (zero past Tk, so those
-    // keys never pass the threshold) and raw V with 1/|v|
-    const int j = k0 + 32 * kh + m;
-    frag kf[NKS], va[NKS];
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      kf[ks] = S::frag(kl, 32 * kh + m, ks, half, DP);
-      va[ks] = S::frag(vl, 32 * kh + m, ks, half, a.D);
-    }
+  for (;;) {
+    const int k0 = cur * kUnit;
+    // S^T: register r -> key k0 + rowof(r, half), lane -> query i
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
     if constexpr (sizeof(T) == 2) {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(kf[ks], qf[ks], s);
-      guard_frags(kf);
+      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(kc[ks], qf[ks], s);
+      guard_frags(kc);
     } else {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s = M::mma(kf[ks], qf[ks], s);
+      for (int ks = 0; ks < NKS; ++ks) s = M::mma(kc[ks], qf[ks], s);
     }
-    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i.  A
-    // conservative gate on the raw products (s > thr), then the exact test
-    // only for registers where some lane passes; only a quadrant with a pair
-    // past the threshold contributes to h.
-    bool anyp = false;
+    // each operand's registers take the next unit's rows as soon as they are
+    // free, so those loads run behind the rest of this unit's work (past the
+    // last unit, the current one again, a cache hit: every iteration then
+    // waits for the same count)
+    const int nxt = walk.next();
+    const int nl = nxt >= 0 ? nxt : cur;
+    load_k(nl, kc);
+    // 1/|v_j| of the lane's key row, to LDS (read back in register order
+    // where a pair passes), then V^T by identity MFMA
+    vzero(vc);
+    {
+      float s2 = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) anyp |= s[r] > thq;
-    if (__ballot(anyp) != 0ull) {
-      // 1/|v_j| in register order
-      float isv[16];
-      {
-        float s2 = 0.0f;
+      for (int ks = 0; ks < NKS; ++ks) s2 = frag_dot(vc[ks], vc[ks], s2);
+      s2 += __shfl_xor(s2, 32);
+      const float iv = inv_len(s2, a.eps);
+      wave_lds_sync();
+      if (half == 0) sv[m] = iv;
+      wave_lds_sync();
+    }
+    frag ta[NDH * NC];
+    frag id[NC];  // formed per unit: fewer registers held across the loop
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) s2 = frag_dot(va[ks], va[ks], s2);
-        s2 += __shfl_xor(s2, 32);
-        const float iv = inv_len(s2, a.eps);
-        wave_lds_sync();
-        if (half == 0) sv[w][m] = iv;
-        wave_lds_sync();
-        read_row_scales(sv[w], half, isv);
-      }
-      // P^T[j][i] = alpha_ij m_ij / |v_j|
-      const int rel0 = i - (k0 + 32 * kh + 8 * half);
+    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = 0.0f;
-        if (__ballot(s[r] > thq) != 0ull) {
-          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-          const float av = trim(s[r] * iq, hp.r);
-          if (av > 0.0f && in_window(dd, hp)) {
-            p = av * av * softmask(dd, hp.iw) * isv[r];
-            if (a.drop.on) p *= dropout_factor(a.drop, bh, i, i - dd);
-          }
+    for (int dblk = 0; dblk < NDH; ++dblk) {
+      f32x16 tr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) tr = M::mma_ng(vc[dblk * NC + c], id[c], tr);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr, c * PER);
+    }
+    guard_frags(vc);
+    guard_frags(id);
+    load_v(nl, vc);
+    // P^T[j][i] = alpha_ij m_ij / |v_j|: a conservative gate on the raw
+    // products (s > thr), the exact test only where some lane passes
+    const int rel0 = i - (k0 + 8 * half);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = 0.0f;
+      if (__ballot(s[r] > thq) != 0ull) {
+        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+        const float av = trim(s[r] * iq, hp.r);
+        if (av > 0.0f && in_window(dd, hp)) {
+          p = av * av * softmask(dd, hp.iw) * sv[rowof(r, half)];
+          if (a.drop.on) p *= dropout_factor(a.drop, bh, i, i - dd);
         }
-        s[r] = p;
       }
-      // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
-      frag pb[NC], ta[NDH * NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) pb[c] = M::pack(s, c * PER);
-      {
-        f32x16 tr[NDH];
-        transpose_rows<T, DP>(va, id, tr);
-#pragma unroll
-        for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-          for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr[dblk], c * PER);
-      }
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int dblk = 0; dblk < NDH; ++dblk) o[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], o[dblk]);
-      guard_frags(ta);
-      guard_frags(pb);
+      s[r] = p;
     }
-    guard_frags(va);
-
+    // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
+    frag pb[NC];
 #pragma unroll
-    for (int n = 0; n < NBUF - 1; ++n) tl[n] = tl[n + 1];
-    tl[NBUF - 1] = walk.next();
+    for (int c = 0; c < NC; ++c) pb[c] = M::pack(s, c * PER);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk) o[dblk] = M::mma_ng(ta[dblk * NC + c], pb[c], o[dblk]);
+    guard_frags(ta);
+    guard_frags(pb);
+    if (nxt < 0) break;
+    cur = nxt;
   }
   guard_frags(qf);
-  guard_frags(id);
-
-  // the kh = 1 wave's H^T reaches the kh = 0 wave through the (now idle)
-  // stage buffers
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(&stage[0][0]);  // [qh][NDH][16][64]
-  if (kh == 1) {
-#pragma unroll
-    for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[((qh * NDH + dblk) * 16 + r) * kWave + lane] = o[dblk][r];
-  }
-  __syncthreads();
-  if (kh == 1) return;
-#pragma unroll
-  for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[dblk][r] += red[((qh * NDH + dblk) * 16 + r) * kWave + lane];
 
   // TanhNorm per query row (lane -> query, registers -> d), y in (B,T,H,D)
   float ss = 0.0f;
@@ -619,7 +623,7 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   if (g.Tk_pad > 0) {
     PrepKArgs pa;
     pa.k = c.k; pa.ks = c.ks; pa.kpm = c.kpm; pa.khat = c.khat;
-    pa.bits = c.bits; pa.bits_per_bh = (int64_t)g.nqt * g.nkt_words;
+    pa.bits = c.bits; pa.bits_per_bh = (int64_t)2 * g.nqt * g.nku_words;
     pa.H = g.H; pa.Tk = g.Tk; pa.D = g.D; pa.Tk_pad = g.Tk_pad; pa.eps = c.eps;
     constexpr int RPB = 256 / (DP * (int)sizeof(T) / 16) * kPrepRows;
     timer_begin(1, c.stream);
@@ -632,7 +636,7 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   FwdKArgs fa;
   fa.q = c.q; fa.qs = c.qs; fa.v = c.v; fa.vs = c.vs; fa.khat = c.khat;
   fa.r = c.r; fa.w = c.w; fa.y = c.y; fa.hnorm = c.hnorm; fa.bits = c.bits;
-  fa.H = g.H; fa.Tq = g.Tq; fa.Tk = g.Tk; fa.D = g.D; fa.nqt = g.nqt; fa.nkt_words = g.nkt_words;
+  fa.H = g.H; fa.Tq = g.Tq; fa.Tk = g.Tk; fa.D = g.D; fa.nqt = g.nqt; fa.nku_words = g.nku_words;
   fa.causal = g.causal; fa.Tk_pad = g.Tk_pad; fa.eps = c.eps; fa.drop = c.drop;
   {
     const int nseg = (g.nkt + ScreenTile<T, DP>::SEG - 1) / ScreenTile<T, DP>::SEG;
@@ -645,8 +649,8 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(3, c.stream);
-  hipLaunchKernelGGL((fwd_live_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream,
-                     fa);
+  hipLaunchKernelGGL((fwd_live_kernel<T, DP>), dim3((unsigned)(2 * g.nqt), (unsigned)(g.B * g.H)), dim3(64), 0,
+                     c.stream, fa);
   timer_end(3, c.stream);
   return hipGetLastError();
 }

@@ -15,7 +15,8 @@ inline int ntiles(int64_t T) { return (int)((T + 63) / 64); }
 
 struct Geometry {
   int B, H, Tq, Tk, D, DP, dtype, causal;
-  int nqt, nkt, nkt_words;
+  int nqt, nkt;
+  int nku_words;  // words per row of the live-unit bitmap (2*nkt 32-key units)
   int64_t Tq_pad, Tk_pad;
   size_t esize;  // bytes per element of dtype
 };

@@ -36,8 +36,10 @@ def test_version_and_sizes():
     # B=4, T=8192, H=8, D=64 bf16: one normalised K^ copy, kept for the backward
     one = 4 * 8 * 8192 * 64 * 2
     assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == one
-    assert L.msa_tile_bits_words(4, 8, 8192, 8192) == 4 * 8 * 128 * 4
-    assert L.msa_tile_bits_words(1, 1, 65, 65) == 2
+    # 2*nqt query-unit rows of ceil(2*nkt/32) words per (b, h)
+    assert L.msa_tile_bits_words(4, 8, 8192, 8192) == 4 * 8 * 256 * 8
+    assert L.msa_tile_bits_words(1, 1, 65, 65) == 4
+    assert L.msa_tile_bits_words(1, 1, 64, 1100) == 2 * 2
     # D=16 is padded to 32 in the workspace
     assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4
     # backward workspace: (dr, dw) partial per (b, h, key tile), then dh
@@ -53,7 +55,7 @@ def test_version_and_sizes():
 def _fwd(L, **kw):
     a = dict(q=16, qs=(1024, 64, 8), k=16, ks=(1024, 64, 8), v=16, vs=(1024, 64, 8),
              B=1, H=8, Tq=16, Tk=16, D=8 * 8, dtype=1, r=16, w=16, kpm=None, causal=1, eps=1e-8,
-             drop=0.0, seed=0, y=16, hnorm=16, bits=16, nbits=8, ws=16, wsb=1 << 30, stream=None)
+             drop=0.0, seed=0, y=16, hnorm=16, bits=16, nbits=16, ws=16, wsb=1 << 30, stream=None)
     a["D"] = 64
     a.update(kw)
     return L.msa_fwd(a["q"], *a["qs"], a["k"], *a["ks"], a["v"], *a["vs"], a["B"], a["H"], a["Tq"],
@@ -93,7 +95,7 @@ def test_fwd_empty_batch_is_a_no_op():
 def test_bwd_and_decode_reject_bad_arguments():
     L = _native.lib()
     rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8, 0.0, 0,
-                   16, 16, 16, 16, 1, 16, 16, 16, 16, 16, 16, 10, None)
+                   16, 16, 16, 16, 2, 16, 16, 16, 16, 16, 16, 10, None)
     assert rc == 2 and "backward workspace" in L.msa_last_error().decode()
     rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8, 0.0, 0,
                    16, 16, 16, 16, 0, 16, 16, 16, 16, 16, 16, 1 << 20, None)

@@ -226,15 +226,19 @@ def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
     D = 64
     q, k, v = correlated_qkv(B, T, T, H, D, seed=4, dtype=torch.float32, rho=0.3)
     y, hnorm, bits = _run_fwd(q, k, v, r, w, True)
-    nW, nA, act = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True)
-    nqt = nkt = T // 64
-    words = (nkt + 31) // 32
-    b = bits.cpu().numpy().view(np.uint32).reshape(B, H, nqt, words)
-    got = np.zeros((B, H, nqt, nkt), dtype=bool)
-    for kt in range(nkt):
-        got[..., kt] = (b[..., kt // 32] >> (kt % 32)) & 1
+    # the bitmap is kept per 32x32 unit: 2*nqt rows of ceil(2*nkt/32) words
+    nW, nA, act = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True, tile=32)
+    _, nA64, act64 = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True, tile=64)
+    nqu = nku = T // 32
+    words = (nku + 31) // 32
+    b = bits.cpu().numpy().view(np.uint32).reshape(B, H, nqu, words)
+    got = np.zeros((B, H, nqu, nku), dtype=bool)
+    for ku in range(nku):
+        got[..., ku] = (b[..., ku // 32] >> (ku % 32)) & 1
     assert nA > 0
     assert np.array_equal(got, act)
+    # a 64x64 tile is live iff one of its four units is
+    assert np.array_equal(got.reshape(B, H, nqu // 2, 2, nku // 2, 2).any(axis=(3, 5)), act64)
 
 
 def test_window_and_threshold_skip_are_exact():
