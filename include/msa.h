@@ -84,7 +84,7 @@ size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
  * ceil(2*nkt/32) words; key unit ku is bit ku%32 of word ku/32 of the row. */
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);
 
-/* Bytes of backward workspace: one (dr, dw) partial per (b, h, 64-key tile),
+/* Bytes of backward workspace: one (dr, dw) partial per (b, h, 32-key unit),
  * summed in a fixed order, plus dh = TanhNorm'(h)^T dy and 1/|q| per query
  * row (padded to 64 rows per tile), which the dQ pass hands to the dK/dV
  * pass. */

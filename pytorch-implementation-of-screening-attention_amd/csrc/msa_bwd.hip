@@ -11,19 +11,22 @@
 //   dq^_i  = sum_j ds_ij k^_j,   dk^_j = sum_i ds_ij q^_i
 //   dr     = -sum 2 a (1-s) m dP,  dw = sum a^2 dP dm/dw
 //   dx     = (dx^ - x^ (x^.dx^)) / |x|   (|x| > eps),  dx^/eps otherwise
-// Only the tiles the forward marked live in its bitmap are revisited; each
-// wave turns its bitmap row/column into a 64-bit ballot mask and walks the set
-// bits.  MFMA operands are the raw q, k, v values (exact in bf16) and the
-// 1/|x| factors are applied in fp32 to the products, so no normalised copy is
+// Only the 32x32 units the forward marked live in its bitmap are revisited;
+// each wave turns its bitmap row/column into a 64-bit ballot mask and walks
+// the set bits.  MFMA operands are the raw q, k, v values (exact in bf16),
+// loaded straight from global memory into operand registers, and the 1/|x|
+// factors are applied in fp32 to the products, so no normalised copy is
 // rounded; dh is formed on the fly from y, dy and |h|.  Operands needed
-// transposed go through a wave-private LDS tile, per-row scale factors
-// through a small LDS vector.  Key padding (attention.py:185-188) enters as a
-// zero 1/|k|, which gives s = 0 and so alpha = 0 for those keys.
+// transposed come from identity MFMAs on the same registers, per-row scale
+// factors reach register order through a small LDS vector.  Key padding
+// (attention.py:185-188) enters as a zero 1/|k|, which gives s = 0 and so
+// alpha = 0 for those keys.
 //
-//   dkdv_kernel     : wave per 64-key tile; accumulates dv^, dk^ in MFMA
-//                     registers over its live query tiles, writes dk, dv and
+//   dq_kernel       : wave per 32-query unit over its live key units; also
+//                     leaves dh and 1/|q| of those rows for dkdv_kernel.
+//   dkdv_kernel     : wave per 32-key unit; accumulates dv^, dk^ in MFMA
+//                     registers over its live query units, writes dk, dv and
 //                     one (dr, dw) partial.
-//   dq_kernel       : wave per 64-query tile over its live key tiles.
 //   rw_reduce_kernel: fixed-order sum of the partials -> dr, dw.
 // No atomics anywhere, so every gradient is bitwise reproducible.
 #include "msa_device.h"
@@ -147,67 +150,59 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[DP / 32], const typena
   });
 }
 
-// Waves per SIMD the backward kernels are register-budgeted for: three (168
-// registers a lane; operands are re-read from LDS rather than held) where the
-// bf16 working set allows, else one.
+// Waves per SIMD the backward kernels are register-budgeted for: two (256
+// registers a lane: the unit's operands, both accumulators and the scaled
+// products all stay in registers) where the bf16 working set allows, else one.
 template <typename T, int DP>
-constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 3 : 1; }
+constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
 
 // ---------------------------------------------------------------------------
-// dQ (runs first).  256-thread block per 64-query tile of head (b,h); wave w
-// works on the quadrant (queries 32*qh .. +31, keys 32*kh .. +31) of every
-// live key tile in the query tile's bitmap row, qh = w/2, kh = w%2.  Lane ->
-// query i = q0 + 32*qh + l32; registers -> keys.  The live key tiles' raw K
-// and V rows are staged into LDS by DMA, double-buffered: tile n+1 streams in
-// while tile n is computed.  K^T comes from an identity MFMA.  Side output for
-// dkdv_kernel: dh (rounded to T, as the operand it becomes) and 1/|q| of every
-// row of a query tile with a live key tile, in the workspace.  The kh = 1
-// wave hands its accumulator to the kh = 0 wave through LDS, which finishes dq.
+// dQ (runs first).  One wave (a 64-thread block) per query unit: 32
+// consecutive queries of head (b,h), lane -> query i = 32*qu + l%32,
+// registers -> keys.  The wave walks its row of the live-unit bitmap; per
+// live key unit it loads the 32 raw K and V rows straight into MFMA operand
+// registers (A operands, row perm_row(l%32)), forms S^T = K Q^T and
+// dP^T = V dH^T, scales them by 1/|k|, 1/|v| (exchanged in register order
+// through a 32-float LDS vector), and accumulates dq^T += K^T (ds/|k|)^T with
+// K^T from an identity MFMA on the same registers.  Side output for
+// dkdv_kernel: dh (rounded to T, as the operand it becomes) and 1/|q| of the
+// unit's rows, written by every unit with a live key unit (the only rows
+// dkdv_kernel reads).
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
-  using S = StageTile<T, DP>;
-  using WS = WaveStage<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  // per wave: DMA ring of its key half of the live key tiles (K rows | V
-  // rows), NBUF buffers, NBUF-1 tiles ahead; waves never wait for each other
-  // inside the tile loop
-  constexpr int NBUF = 1;  // a small LDS footprint leaves room for three blocks per CU
-  __shared__ __attribute__((aligned(16))) char stage[4][NBUF][2 * WS::TILEB];
-  static_assert(2 * NDH * 16 * kWave * 4 <= 4 * NBUF * 2 * WS::TILEB, "exchange must fit the stage buffers");
-  __shared__ __attribute__((aligned(16))) float sk[4][32];                 // per wave: 1/|k| (0 if masked)
-  __shared__ __attribute__((aligned(16))) float sv[4][32];              // per wave: 1/|v|
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
-  const int half = lane >> 5, l32 = lane & 31;
-  int qt, bh;
-  xcd_interleave(qt, bh);
+  __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k| (0 if padded or masked) of the unit's key rows
+  __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v|
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  int qu, bh;
+  xcd_interleave(qu, bh);
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);
-  const int q0 = qt * kTile;
-  const int i = q0 + 32 * qh + l32;
+  const int i = qu * kUnit + l32;
   const bool valid = i < a.Tq;
   const int ii = valid ? i : 0;
   T* dqrow = (T*)a.dq + (((int64_t)b * a.Tq + ii) * a.H + h) * a.D;
 
-  const int64_t qlast = q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1;
-  int64_t jlo = (int64_t)q0 - hp.wc + 1;
-  int64_t jhi = causal ? qlast : qlast + hp.wc - 1;
-  if (jlo < 0) jlo = 0;
-  if (jhi > a.Tk - 1) jhi = a.Tk - 1;
-  const int kt_lo = (int)(jlo / kTile), kt_hi = jhi >= jlo ? (int)(jhi / kTile) : kt_lo - 1;
-  // key tile kl is live for this query tile iff one of its four 32x32 units
-  // is: bits 2kl, 2kl+1 of the rows of query units 2qt, 2qt+1
-  const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + 2 * qt) * a.nku_words;
-  const int nw = a.nku_words;
-  auto bitf = [brow, nw](int kl) { return (((brow[kl >> 4] | brow[nw + (kl >> 4)]) >> ((2 * kl) & 31)) & 3u) != 0u; };
-  BitWalk<decltype(bitf)> walk(bitf, kt_lo, kt_hi);
+  int ku_lo, ku_hi;
+  {
+    const int64_t qa = (int64_t)qu * kUnit, qb = qa + kUnit - 1 < a.Tq - 1 ? qa + kUnit - 1 : a.Tq - 1;
+    int64_t jlo = qa - hp.wc + 1;
+    int64_t jhi = causal ? qb : qb + hp.wc - 1;
+    if (jlo < 0) jlo = 0;
+    if (jhi > a.Tk - 1) jhi = a.Tk - 1;
+    ku_lo = (int)(jlo / kUnit);
+    ku_hi = jhi >= jlo ? (int)(jhi / kUnit) : ku_lo - 1;
+  }
+  const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + qu) * a.nku_words;
+  auto bitf = [brow](int u) { return ((brow[u >> 5] >> (u & 31)) & 1u) != 0u; };
+  BitWalk<decltype(bitf)> walk(bitf, ku_lo, ku_hi);
   int cur = walk.next();
-  if (cur < 0) {  // block-uniform: no live key tile, dq = 0
-    if (kh == 0 && valid)
+  if (cur < 0) {  // wave-uniform: no live key unit, dq = 0
+    if (valid)
 #pragma unroll
       for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
@@ -218,32 +213,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
     return;
   }
 
-  const T* krow0 = (const T*)a.k + b * a.ks.sb + h * a.ks.sh;
-  const T* vrow0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
+  // key row of this lane in unit u: 32u + perm_row(l32), read as row Tk-1
+  // past Tk (its 1/|k| is then 0, so it contributes nothing); the lane's
+  // chunks from a wave-uniform row base plus a 32-bit lane offset
   const int m = perm_row(l32);
-  // the DMA offsets are formed at each issue from a laundered lane index, so
-  // the compiler keeps no per-lane offsets live across the tile loop
-  auto stage_tile = [&](int kt, int buf, uint8_t& msk) {
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const auto plk = WS::plan(a.ks.st, a.D, ln), plv = WS::plan(a.vs.st, a.D, ln);
-    WS::issue(plk, krow0, a.ks.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf], ln, 0);
-    WS::issue(plv, vrow0, a.vs.st, (int64_t)kt * kTile + 32 * kh, a.Tk, a.D, stage[w][buf] + WS::TILEB, ln, 0);
-    const int j = kt * kTile + 32 * kh + m;
-    msk = (a.kpm != nullptr && j < a.Tk) ? a.kpm[(int64_t)b * a.Tk + j] : (uint8_t)0;
+  const T* kb0 = (const T*)a.k + b * a.ks.sb + h * a.ks.sh;
+  const T* vb0 = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
+  auto load_rows = [&](const T* base, int64_t st, int u, frag (&f)[NKS]) {
+    const int r = u * kUnit + m < a.Tk ? m : a.Tk - 1 - u * kUnit;
+    const uint32_t off = (uint32_t)(((int64_t)r * st + PER * half) * (int64_t)sizeof(T));
+    const char* p = (const char*)(base + (int64_t)u * kUnit * st) + off;
+    // chunks past D (D = 16 < DP = 32 only) re-read chunk 0; zero_tail clears them
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int c = DP == 32 && KS * ks >= a.D ? 0 : KS * ks;
+      f[ks] = M::load((const T*)(p + c * (int)sizeof(T)));
+    }
   };
-  // tl[n]: the n-th next live key tile (-1 past the end); mk[n] its key-padding byte
-  int tl[3] = {cur, -1, -1};
-  uint8_t mk[3] = {0, 0, 0};
-  // own queries' rows first, then the first key tiles' DMA behind them
-  // (vector memory returns in order, so the rows are not held up by the DMA)
-  frag qb[NKS], hb[NKS];
+  auto zero_tail = [&](frag (&f)[NKS]) {
+    if constexpr (DP == 32) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        if (KS * ks >= a.D) f[ks] = M::zero();
+    }
+  };
+  // 1/|k| is 0 for keys past Tk and for masked keys
+  auto key_ok = [&](int u) {
+    const int j = u * kUnit + m;
+    return j < a.Tk && !(a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + j] != 0);
+  };
+
+  // own queries' rows first, then the first key unit's rows behind them
+  frag qb[NKS], hb[NKS], kc[NKS], vc[NKS];
   float iql;
+  bool kok;
   {
     QueryRows<T, DP> qr;
     qr.load(a, b, h, bh, i, half);
-    stage_tile(tl[0], 0, mk[0]);
-    tl[1] = walk.next();
+    load_rows(kb0, a.ks.st, cur, kc);
+    load_rows(vb0, a.vs.st, cur, vc);
+    kok = key_ok(cur);
     iql = qr.finish(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
@@ -251,7 +260,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
       hb[ks] = qr.dh.f[ks];
     }
   }
-  if (kh == 0) {  // dh and 1/|q| of this tile's rows for dkdv_kernel (zero past Tq)
+  {  // dh and 1/|q| of this unit's rows for dkdv_kernel (zero past Tq)
     T* dst = (T*)a.dh + ((int64_t)bh * a.Tq_pad + i) * DP;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) *reinterpret_cast<frag*>(dst + KS * ks + PER * half) = hb[ks];
@@ -264,267 +273,213 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
 #pragma unroll
     for (int r = 0; r < 16; ++r) adq[dblk][r] = 0.0f;
 
-  for (int it = 0; tl[0] >= 0; ++it) {
-    // this wave's DMA of tile tl[0] is complete
-    wait_vmcnt<0>();
-    wave_lds_sync();
-    const char* kl = stage[w][0];
-    const char* vl = kl + WS::TILEB;
-    const int k0 = tl[0] * kTile;
-    const uint8_t mk_cur = mk[0];
-
-    // key rows j = k0 + 32*kh + perm_row(l32) as A operands.  S^T = K Q^T and
-    // dP^T = V dH^T take one operand set at a time (fragments re-read from
-    // LDS when needed again), with the rows' squared norms from the same
-    // fragments.
-    const int j = k0 + 32 * kh + m;
-    const bool jok = j < a.Tk;
+  for (;;) {
+    const int k0 = cur * kUnit;
+    zero_tail(kc);
+    zero_tail(vc);
+    // register r -> key k0 + rowof(r, half), lane -> query i
     f32x16 s, dp;
     float s2k = 0.0f, s2v = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
-    {
-      frag f[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) f[ks] = WS::frag(kl, m, ks, half, a.D);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        s = M::mma_ng(f[ks], qb[ks], s);
-        s2k = frag_dot(f[ks], f[ks], s2k);
-      }
-      guard_frags(f);
+    for (int ks = 0; ks < NKS; ++ks) {
+      s = M::mma_ng(kc[ks], qb[ks], s);
+      s2k = frag_dot(kc[ks], kc[ks], s2k);
     }
-    {
-      frag f[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) f[ks] = WS::frag(vl, m, ks, half, a.D);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        dp = M::mma_ng(f[ks], hb[ks], dp);
-        s2v = frag_dot(f[ks], f[ks], s2v);
-      }
-      guard_frags(f);
+    for (int ks = 0; ks < NKS; ++ks) {
+      dp = M::mma_ng(vc[ks], hb[ks], dp);
+      s2v = frag_dot(vc[ks], vc[ks], s2v);
     }
+    guard_frags(vc);
+    const int nxt = walk.next();
     s2k += __shfl_xor(s2k, 32);
     s2v += __shfl_xor(s2v, 32);
     {
-      const float ik = (jok && mk_cur == 0) ? inv_len(s2k, a.eps) : 0.0f;  // 0 if padded or masked
+      const float ik = kok ? inv_len(s2k, a.eps) : 0.0f;
       const float iv = inv_len(s2v, a.eps);
       wave_lds_sync();
-      if (half == 0) { sk[w][m] = ik; sv[w][m] = iv; }
+      if (half == 0) { sk[m] = ik; sv[m] = iv; }
       wave_lds_sync();
     }
-    // register r -> key k0 + 32kh + rowof(r, half), lane -> query i.  Scaled
-    // in place: s = (q . k)/|k|, dp = dH . v^.
+    // scaled in place: s = (q . k)/|k|, dp = dH . v^
     {
       float sc[16];
-      read_row_scales(sk[w], half, sc);
+      read_row_scales(sk, half, sc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] *= sc[r];
-      read_row_scales(sv[w], half, sc);
+      read_row_scales(sv, half, sc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
     }
-    // A conservative gate on the products (s > thr |q|), then the exact test
-    // only for registers where some lane passes; only a quadrant with a pair
-    // past the threshold contributes to dq.
-    bool anyp = false;
+    // a conservative gate on the products (s > thr |q|), then the exact
+    // test only for registers where some lane passes
+    const int rel0 = i - (k0 + 8 * half);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) anyp |= s[r] > thq;
-    if (__ballot(anyp) != 0ull) {
-      const int rel0 = i - (k0 + 32 * kh + 8 * half);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float ds = 0.0f;
-        if (__ballot(s[r] > thq) != 0ull) {
-          const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-          const float av = trim(s[r] * iql, hp.r);
-          if (av > 0.0f && valid && in_window(dd, hp)) {
-            ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r];
-            if (a.drop.on) ds *= dropout_factor(a.drop, bh, i, i - dd);
-          }
+    for (int r = 0; r < 16; ++r) {
+      float ds = 0.0f;
+      if (__ballot(s[r] > thq) != 0ull) {
+        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+        const float av = trim(s[r] * iql, hp.r);
+        if (av > 0.0f && valid && in_window(dd, hp)) {
+          ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r];
+          if (a.drop.on) ds *= dropout_factor(a.drop, bh, i, i - dd);
         }
-        dp[r] = ds;
-        __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
       }
-      // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
-      // the key rows, one 32-column block of d at a time
-      {
-        float sc[16];
-        read_row_scales(sk[w], half, sc);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
-      }
-      frag db[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
-#pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk) {
-        frag f[NC], kt[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) f[c] = WS::frag(kl, m, dblk * NC + c, half, a.D);
-        f32x16 tr;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) tr = M::mma_ng(f[c], ident_frag<T>(c, lane), tr);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) kt[c] = M::pack(tr, c * PER);
-        guard_frags(f);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) adq[dblk] = M::mma_ng(kt[c], db[c], adq[dblk]);
-        guard_frags(kt);
-      }
-      guard_frags(db);
+      dp[r] = ds;
+      __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
     }
-
-    // every LDS read of this tile is done: its buffer takes the next tile
-    wave_lds_sync();
-    if (tl[1] >= 0) stage_tile(tl[1], 0, mk[1]);
-    tl[0] = tl[1];
-    mk[0] = mk[1];
-    tl[1] = walk.next();
+    // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
+    // the key rows, one 32-column block of d at a time
+    {
+      float sc[16];
+      read_row_scales(sk, half, sc);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
+    }
+    frag db[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk) {
+      frag kt[NC];
+      f32x16 tr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) tr = M::mma_ng(kc[dblk * NC + c], ident_frag<T>(c, lane), tr);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kt[c] = M::pack(tr, c * PER);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) adq[dblk] = M::mma_ng(kt[c], db[c], adq[dblk]);
+      guard_frags(kt);
+    }
+    guard_frags(kc);
+    guard_frags(db);
+    if (nxt < 0) break;
+    cur = nxt;
+    load_rows(kb0, a.ks.st, cur, kc);
+    load_rows(vb0, a.vs.st, cur, vc);
+    kok = key_ok(cur);
   }
   guard_frags(qb);
   guard_frags(hb);
-
-  // the kh = 1 wave's accumulator reaches the kh = 0 wave through the
-  // (now idle) stage buffers
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(&stage[0][0][0]);  // [qh][NDH][16][64]
-  if (kh == 1) {
-#pragma unroll
-    for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[((qh * NDH + dblk) * 16 + r) * kWave + lane] = adq[dblk][r];
-  }
-  __syncthreads();
-  if (kh == 0) {
-#pragma unroll
-    for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) adq[dblk][r] += red[((qh * NDH + dblk) * 16 + r) * kWave + lane];
-    write_norm_bwd<T, DP>(adq, qb, valid, a.D, a.eps, half, dqrow);
-  }
+  write_norm_bwd<T, DP>(adq, qb, valid, a.D, a.eps, half, dqrow);
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV (runs after dq_kernel).  256-thread block per 64-key tile of head
-// (b,h); wave w works on the quadrant (keys 32*kh .. +31, queries
-// 32*qh .. +31) of every live query tile in the key tile's bitmap column,
-// kh = w%2, qh = w/2, so the two waves of a key half accumulate over
-// different query halves.  Lane -> key j = k0 + 32*kh + l32 of the C blocks;
-// registers -> queries.  Per live query tile, its raw Q rows, the dh rows and
-// 1/|q| that dq_kernel left in the workspace are staged into LDS by DMA,
-// double-buffered.  The transposed Q^T and dH^T operands of the dK/dV products
-// are formed by identity MFMAs.  At the end the two waves of a key half
-// exchange one accumulator through LDS: the qh = 0 wave finishes dk, the
-// qh = 1 wave finishes dv.
+// dK, dV (runs after dq_kernel).  One wave (a 64-thread block) per key unit:
+// 32 consecutive keys of head (b,h), lane -> key j = 32*ku + l%32 of the C
+// blocks, registers -> queries.  The wave walks its column of the live-unit
+// bitmap; per live query unit it loads the raw Q rows and the dh rows and
+// 1/|q| that dq_kernel left in the workspace straight into MFMA operand
+// registers (A operands, row perm_row(l%32)), forms S = Q K^T and dP = dH V^T
+// with its own raw K, V rows as B operands, and accumulates
+// dv^T += dH^T P and dk^T += Q^T (ds/|q|) with dH^T, Q^T from identity MFMAs
+// on the same registers.  1/|q| reaches register order through a 32-float
+// LDS vector.  The wave finishes dk, dv and its (dr, dw) partial.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dkdv_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dkdv_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
-  using S = StageTile<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  constexpr int SB = 2 * S::TILEB + 1024;  // per buffer: Q tile | dh tile | 1/|q| (64 floats, 1 KB slot)
-  constexpr int KVB = 2 * NKS * kWave * (int)sizeof(frag);  // per key half: own K, V fragments
-  // DMA ring of staged query tiles: NBUF buffers, NBUF-1 tiles ahead where LDS allows
-  // (two buffers for bf16 at D <= 64 keep the block under a third of the LDS,
-  // for three blocks per CU)
-  constexpr int NBUF = bwd_waves<T, DP>() == 3 ? 2
-                       : (3 * SB + 2 * KVB <= 70 * 1024 ? 3 : (2 * SB + 2 * KVB <= 150 * 1024 ? 2 : 1));
-  constexpr int PT = 2 * S::CPT;  // DMA operations per thread per tile (wave 0 issues one more)
-  static_assert(4 * NDH * 16 * kWave * 4 <= NBUF * SB, "exchange must fit the stage buffers");
-  __shared__ __attribute__((aligned(16))) char stage[NBUF][SB];
-  __shared__ __attribute__((aligned(16))) char kvs[2][KVB];
-  __shared__ float rw[2][4];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), kh = w & 1, qh = w >> 1;
-  const int half = lane >> 5, l32 = lane & 31;
-  int kt, bh;
-  xcd_interleave(kt, bh);
-  // a key tile's live query tiles lie after it (its window runs forward), so
-  // under a causal mask the lowest key tiles carry the most work: they go first
-  if (a.causal) kt = (int)gridDim.x - 1 - kt;
+  __shared__ __attribute__((aligned(16))) float sq[32];  // 1/|q| of the current query unit's rows
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  int ku, bh;
+  xcd_interleave(ku, bh);
+  // a key unit's live query units lie after it (its window runs forward), so
+  // under a causal mask the lowest key units carry the most work: they go first
+  if (a.causal) ku = (int)gridDim.x - 1 - ku;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);
-  const int k0 = kt * kTile;
-  const int j = k0 + 32 * kh + l32;
+  const int k0 = ku * kUnit;
+  const int j = k0 + l32;
   const bool jvalid = j < a.Tk;
   const int jj = jvalid ? j : 0;
   const int64_t orow = (((int64_t)b * a.Tk + jj) * a.H + h) * a.D;
+  const int64_t nbh = (int64_t)a.B * a.H;
+  const int nku = 2 * a.nkt;
 
-  const int64_t klast = k0 + 63 < a.Tk - 1 ? k0 + 63 : a.Tk - 1;
-  int64_t ilo = causal ? (int64_t)k0 : (int64_t)k0 - hp.wc + 1;
-  int64_t ihi = klast + hp.wc - 1;
-  if (ilo < 0) ilo = 0;
-  if (ihi > a.Tq - 1) ihi = a.Tq - 1;
-  const int qt_lo = (int)(ilo / kTile), qt_hi = ihi >= ilo ? (int)(ihi / kTile) : qt_lo - 1;
-  // query tile ql is live for this key tile iff one of its four 32x32 units
-  // is: bits 2kt, 2kt+1 of the rows of query units 2ql, 2ql+1
-  const uint32_t* bcol = a.bits + (int64_t)bh * 2 * a.nqt * a.nku_words + (kt >> 4);
-  const int nw = a.nku_words, sh = (2 * kt) & 31;
-  auto bitf = [bcol, nw, sh](int ql) {
-    return (((bcol[(int64_t)2 * ql * nw] | bcol[(int64_t)(2 * ql + 1) * nw]) >> sh) & 3u) != 0u;
-  };
-  BitWalk<decltype(bitf)> walk(bitf, qt_lo, qt_hi);
+  int qu_lo, qu_hi;
+  {
+    const int64_t klast = k0 + kUnit - 1 < a.Tk - 1 ? k0 + kUnit - 1 : a.Tk - 1;
+    int64_t ilo = causal ? (int64_t)k0 : (int64_t)k0 - hp.wc + 1;
+    int64_t ihi = klast + hp.wc - 1;
+    if (ilo < 0) ilo = 0;
+    if (ihi > a.Tq - 1) ihi = a.Tq - 1;
+    qu_lo = (int)(ilo / kUnit);
+    qu_hi = ihi >= ilo && k0 < a.Tk ? (int)(ihi / kUnit) : qu_lo - 1;
+  }
+  const uint32_t* bcol = a.bits + (int64_t)bh * 2 * a.nqt * a.nku_words + (ku >> 5);
+  const int nw = a.nku_words, sh = ku & 31;
+  auto bitf = [bcol, nw, sh](int qu) { return ((bcol[(int64_t)qu * nw] >> sh) & 1u) != 0u; };
+  BitWalk<decltype(bitf)> walk(bitf, qu_lo, qu_hi);
   int cur = walk.next();
-  if (cur < 0) {  // block-uniform: no live query tile, dk = dv = 0
-    T* out = (T*)(qh == 0 ? a.dk : a.dv) + orow;
+  if (cur < 0) {  // wave-uniform: no live query unit, dk = dv = 0
     if (jvalid)
 #pragma unroll
       for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = 32 * dblk + 8 * g + 4 * half;
-          if (d < a.D) store4(out + d, 0.0f, 0.0f, 0.0f, 0.0f);
+          if (d < a.D) {
+            store4((T*)a.dk + orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+            store4((T*)a.dv + orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
+          }
         }
-    if (tid == 0) {
-      const int64_t nbh = (int64_t)a.B * a.H;
-      a.part[(int64_t)bh * a.nkt + kt] = 0.0f;
-      a.part[nbh * a.nkt + (int64_t)bh * a.nkt + kt] = 0.0f;
+    if (lane == 0) {
+      a.part[(int64_t)bh * nku + ku] = 0.0f;
+      a.part[nbh * nku + (int64_t)bh * nku + ku] = 0.0f;
     }
     return;
   }
 
-  const T* qrow0 = (const T*)a.q + b * a.qs.sb + h * a.qs.sh;
-  const T* dh0 = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
+  // query row of this lane in unit u: 32u + perm_row(l32).  Raw q rows past
+  // Tq read row Tq-1; their 1/|q| and dh rows (workspace, zero past Tq) are
+  // 0, so they contribute nothing.  A wave-uniform row base plus a 32-bit
+  // lane offset per operand.
+  const int m = perm_row(l32);
+  const T* qb0 = (const T*)a.q + b * a.qs.sb + h * a.qs.sh;
+  const T* hb0 = (const T*)a.dh + (int64_t)bh * a.Tq_pad * DP;
   const float* iq0 = a.iqs + (int64_t)bh * a.Tq_pad;
-  // DMA offsets formed at each issue from a laundered thread index (nothing
-  // per-lane kept live across the tile loop)
-  auto stage_tile = [&](int qt, int buf) {
-    int tx = tid;
-    asm volatile("" : "+v"(tx));
-    const auto plq = S::plan(a.qs.st, a.D, tx), plh = S::plan(DP, DP, tx);
-    S::issue(plq, qrow0, a.qs.st, (int64_t)qt * kTile, a.Tq, a.D, stage[buf], tx, w);
-    S::issue(plh, dh0, DP, (int64_t)qt * kTile, a.Tq_pad, DP, stage[buf] + S::TILEB, tx, w);
-    if (w == 0)  // 64 floats of 1/|q|: lanes 0-15 carry them, the rest repeat lane 15 into the slot's tail
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(iq0 + (int64_t)qt * kTile + 4 * (lane < 16 ? lane : 15)),
-          (void __attribute__((address_space(3)))*)(stage[buf] + 2 * S::TILEB), 16, 0, 0);
+  auto load_unit = [&](int u, frag (&qf)[NKS], frag (&hf)[NKS], float& iqv) {
+    const int r = u * kUnit + m < a.Tq ? m : a.Tq - 1 - u * kUnit;
+    const uint32_t qoff = (uint32_t)(((int64_t)r * a.qs.st + PER * half) * (int64_t)sizeof(T));
+    const char* pq = (const char*)(qb0 + (int64_t)u * kUnit * a.qs.st) + qoff;
+    const char* ph = (const char*)(hb0 + (int64_t)u * kUnit * DP) + (uint32_t)((m * DP + PER * half) * (int)sizeof(T));
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int c = DP == 32 && KS * ks >= a.D ? 0 : KS * ks;  // chunks past D re-read chunk 0 (cleared at use)
+      qf[ks] = M::load((const T*)(pq + c * (int)sizeof(T)));
+      hf[ks] = M::load((const T*)(ph + KS * ks * (int)sizeof(T)));
+    }
+    iqv = iq0[(int64_t)u * kUnit + l32];  // lanes l and l+32 read the same row
   };
-  // tl[n]: the n-th next live query tile (-1 past the end)
-  int tl[3] = {cur, -1, -1};
-  // own keys as raw B operands (lane -> key), kept in LDS (one copy per key
-  // half, written by its qh = 0 wave before the loop's first barrier), with
-  // 1/|k| (0 if padded or masked) and 1/|v|.  Their loads go first, the first
-  // query tile's DMA behind them (vector memory returns in order).
-  frag* kvl = reinterpret_cast<frag*>(kvs[kh]);
-  float ikl, ivl;
+  auto zero_tail = [&](frag (&f)[NKS]) {
+    if constexpr (DP == 32) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        if (KS * ks >= a.D) f[ks] = M::zero();
+    }
+  };
+
+  // own keys as raw B operands (lane -> key) with 1/|k| (0 if padded or
+  // masked) and 1/|v|; their loads go first, the first query unit's behind
+  frag kb[NKS], vb[NKS], qf[NKS], hf[NKS];
+  float ikl, ivl, iqv;
   {
     KeyRows<T, DP> kr;
     kr.load(a, b, h, j, half);
-    stage_tile(tl[0], 0);
-    for (int n = 1; n < (NBUF > 1 ? NBUF : 2); ++n) tl[n] = walk.next();
+    load_unit(cur, qf, hf, iqv);
     kr.finish(a.eps, ikl, ivl);
-    if (qh == 0)
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        kvl[ks * kWave + lane] = kr.k.f[ks];
-        kvl[(NKS + ks) * kWave + lane] = kr.v.f[ks];
-      }
+    for (int ks = 0; ks < NKS; ++ks) {
+      kb[ks] = kr.k.f[ks];
+      vb[ks] = kr.v.f[ks];
+    }
   }
   f32x16 acc_k[NDH], acc_v[NDH];
 #pragma unroll
@@ -532,183 +487,116 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
 #pragma unroll
     for (int r = 0; r < 16; ++r) { acc_k[dblk][r] = 0.0f; acc_v[dblk][r] = 0.0f; }
   float dr_acc = 0.0f, dw_acc = 0.0f;
-  const int m = perm_row(l32);
   const float thk = hp.thr / ikl;  // s > thr  <=>  (q . k)/|q| > thr |k|  (+inf for masked keys)
 
-  if (NBUF == 3 && tl[1] >= 0) stage_tile(tl[1], 1);
-  for (int it = 0; tl[0] >= 0; ++it) {
-    // tile tl[0] is in LDS once this wave's older DMA is done and every wave
-    // passed the barrier; the buffer refilled next was read last iteration
-    if (NBUF == 3 && tl[1] >= 0) wait_vmcnt<PT>();
-    else wait_vmcnt<0>();
-    block_sync_lds();
-    if (NBUF > 1 && tl[NBUF - 1] >= 0) stage_tile(tl[NBUF - 1], (it + NBUF - 1) % NBUF);
-    const char* ql = stage[it % NBUF];
-    const char* hl = ql + S::TILEB;
-    const float* iql = reinterpret_cast<const float*>(ql + 2 * S::TILEB);
-    const int q0 = tl[0] * kTile;
-
-    // query rows i = q0 + 32*qh + perm_row(l32) as A operands: raw q, dh
-    // (rows past Tq carry 1/|q| = 0 and dh = 0, so they contribute nothing).
-    // S = Q K^T and dP = dH V^T take one operand pair at a time; the
-    // fragments are re-read from LDS where needed again.
+  for (;;) {
+    const int q0 = cur * kUnit;
+    zero_tail(qf);
+    wave_lds_sync();
+    if (half == 0) sq[l32] = iqv;
+    wave_lds_sync();
+    // register r -> query q0 + rowof(r, half), lane -> key j.  Scaled in
+    // place: s = (q . k)/|q|, dp = (dh . v)/|v|.
     f32x16 s, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
-    {
-      frag f[NKS], g[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        f[ks] = S::frag(ql, 32 * qh + m, ks, half, a.D);
-        g[ks] = kvl[ks * kWave + lane];
-      }
+    for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(qf[ks], kb[ks], s);
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(f[ks], g[ks], s);
-      guard_frags(f);
-      guard_frags(g);
-    }
-    {
-      frag f[NKS], g[NKS];
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        f[ks] = S::frag(hl, 32 * qh + m, ks, half, DP);
-        g[ks] = kvl[(NKS + ks) * kWave + lane];
-      }
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) dp = M::mma_ng(f[ks], g[ks], dp);
-      guard_frags(f);
-      guard_frags(g);
-    }
-    // register r -> query q0 + 32qh + rowof(r, half), lane -> key j.  Scaled
-    // in place: s = (q . k)/|q|, dp = (dh . v)/|v|.
+    for (int ks = 0; ks < NKS; ++ks) dp = M::mma_ng(hf[ks], vb[ks], dp);
+    const int nxt = walk.next();
     {
       float sc[16];
-      read_row_scales(iql + 32 * qh, half, sc);
+      read_row_scales(sq, half, sc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s[r] *= sc[r];
         dp[r] *= ivl;
       }
     }
-
-    // A conservative gate on the products (s > thr |k|), then the exact test
-    // only for registers where some lane passes; only a quadrant with a pair
-    // past the threshold contributes to dk, dv, dr, dw.
-    bool anyp = false;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) anyp |= s[r] > thk;
-    if (__ballot(anyp) != 0ull) {
-      const int rel0 = (q0 + 32 * qh + 8 * half) - j;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = 0.0f, ds = 0.0f;
-        if (__ballot(s[r] > thk) != 0ull) {
-          const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-          const float sv = s[r] * ikl;
-          const float av = trim(sv, hp.r);
-          if (av > 0.0f && in_window(dd, hp)) {
-            const float c = a.drop.on ? dropout_factor(a.drop, bh, j + dd, j) : 1.0f;
-            const float mk = softmask(dd, hp.iw) * c;
-            const float g = dp[r];
-            p = av * av * mk;
-            ds = 2.0f * av * hp.r * mk * g;
-            dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
-            dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
-          }
-        }
-        s[r] = p;
-        dp[r] = ds;
-        __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
-      }
-      {
-        float sc[16];
-        read_row_scales(iql + 32 * qh, half, sc);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dp[r] *= sc[r];  // ds/|q|
-      }
-      // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
-      // with dH^T, Q^T from identity products on re-read rows, one 32-column
-      // block of d at a time
-      frag pb[NC], db[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        pb[c] = M::pack(s, c * PER);
-        db[c] = M::pack(dp, c * PER);
-      }
-#pragma unroll
-      for (int dblk = 0; dblk < NDH; ++dblk) {
-#pragma unroll
-        for (int op = 0; op < 2; ++op) {  // 0: dH^T P -> dv, 1: Q^T dS -> dk
-          frag f[NC], t[NC];
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-            f[c] = op == 0 ? S::frag(hl, 32 * qh + m, dblk * NC + c, half, DP)
-                           : S::frag(ql, 32 * qh + m, dblk * NC + c, half, a.D);
-          f32x16 tr;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
-#pragma unroll
-          for (int c = 0; c < NC; ++c) tr = M::mma_ng(f[c], ident_frag<T>(c, lane), tr);
-#pragma unroll
-          for (int c = 0; c < NC; ++c) t[c] = M::pack(tr, c * PER);
-          guard_frags(f);
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            if (op == 0) acc_v[dblk] = M::mma_ng(t[c], pb[c], acc_v[dblk]);
-            else acc_k[dblk] = M::mma_ng(t[c], db[c], acc_k[dblk]);
-          }
-          guard_frags(t);
-        }
-      }
-      guard_frags(pb);
-      guard_frags(db);
-    }
-
-    if (NBUF == 1 && tl[1] >= 0) {
-      block_sync_lds();  // every wave is done with the single buffer
-      stage_tile(tl[1], 0);
-    }
-    tl[0] = tl[1];
-    tl[1] = tl[2];
-    tl[2] = NBUF == 3 ? walk.next() : -1;
-    if (NBUF < 3) tl[1] = walk.next();
-  }
-
-  // exchange through the (now idle) stage buffers: the qh = 0 wave of each
-  // key half finishes dk, the qh = 1 wave dv
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(&stage[0][0]);  // [4 waves][NDH][16][64]
-#pragma unroll
-  for (int dblk = 0; dblk < NDH; ++dblk)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      red[((w * NDH + dblk) * 16 + r) * kWave + lane] = qh == 0 ? acc_v[dblk][r] : acc_k[dblk][r];
-  dr_acc = wave_sum(dr_acc);
-  dw_acc = wave_sum(dw_acc);
-  if (lane == 0) { rw[0][w] = dr_acc; rw[1][w] = dw_acc; }
-  __syncthreads();
-  f32x16 fin[NDH];
-#pragma unroll
-  for (int dblk = 0; dblk < NDH; ++dblk)
+    // a conservative gate on the products (s > thr |k|), then the exact
+    // test only for registers where some lane passes
+    const int rel0 = (q0 + 8 * half) - j;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float other = red[(((w ^ 2) * NDH + dblk) * 16 + r) * kWave + lane];
-      fin[dblk][r] = qh == 0 ? acc_k[dblk][r] + other : other + acc_v[dblk][r];
+      float p = 0.0f, ds = 0.0f;
+      if (__ballot(s[r] > thk) != 0ull) {
+        const int dd = rel0 + 16 * (r >> 3) + (r & 7);
+        const float sv = s[r] * ikl;
+        const float av = trim(sv, hp.r);
+        if (av > 0.0f && in_window(dd, hp)) {
+          const float c = a.drop.on ? dropout_factor(a.drop, bh, j + dd, j) : 1.0f;
+          const float mk = softmask(dd, hp.iw) * c;
+          const float g = dp[r];
+          p = av * av * mk;
+          ds = 2.0f * av * hp.r * mk * g;
+          dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
+          dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
+        }
+      }
+      s[r] = p;
+      dp[r] = ds;
+      __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
     }
-  {
-    frag xf[NKS];  // own raw k (qh = 0) or v (qh = 1) rows, from LDS
+    {
+      float sc[16];
+      read_row_scales(sq, half, sc);
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) xf[ks] = kvl[(qh * NKS + ks) * kWave + lane];
-    write_norm_bwd<T, DP>(fin, xf, jvalid, a.D, a.eps, half, (T*)(qh == 0 ? a.dk : a.dv) + orow);
+      for (int r = 0; r < 16; ++r) dp[r] *= sc[r];  // ds/|q|
+    }
+    // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
+    // with dH^T, Q^T from identity products on the row registers, one
+    // 32-column block of d at a time
+    frag pb[NC], db[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      pb[c] = M::pack(s, c * PER);
+      db[c] = M::pack(dp, c * PER);
+    }
+#pragma unroll
+    for (int dblk = 0; dblk < NDH; ++dblk) {
+#pragma unroll
+      for (int op = 0; op < 2; ++op) {  // 0: dH^T P -> dv, 1: Q^T dS -> dk
+        frag t[NC];
+        f32x16 tr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          tr = M::mma_ng(op == 0 ? hf[dblk * NC + c] : qf[dblk * NC + c], ident_frag<T>(c, lane), tr);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) t[c] = M::pack(tr, c * PER);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if (op == 0) acc_v[dblk] = M::mma_ng(t[c], pb[c], acc_v[dblk]);
+          else acc_k[dblk] = M::mma_ng(t[c], db[c], acc_k[dblk]);
+        }
+        guard_frags(t);
+      }
+    }
+    guard_frags(qf);
+    guard_frags(hf);
+    guard_frags(pb);
+    guard_frags(db);
+    if (nxt < 0) break;
+    cur = nxt;
+    load_unit(cur, qf, hf, iqv);
   }
-  if (tid == 0) {
-    const int64_t nbh = (int64_t)a.B * a.H;
-    a.part[(int64_t)bh * a.nkt + kt] = (rw[0][0] + rw[0][1]) + (rw[0][2] + rw[0][3]);
-    a.part[nbh * a.nkt + (int64_t)bh * a.nkt + kt] = (rw[1][0] + rw[1][1]) + (rw[1][2] + rw[1][3]);
+  guard_frags(kb);
+  guard_frags(vb);
+
+  write_norm_bwd<T, DP>(acc_k, kb, jvalid, a.D, a.eps, half, (T*)a.dk + orow);
+  write_norm_bwd<T, DP>(acc_v, vb, jvalid, a.D, a.eps, half, (T*)a.dv + orow);
+  dr_acc = wave_sum(dr_acc);
+  dw_acc = wave_sum(dw_acc);
+  if (lane == 0) {
+    a.part[(int64_t)bh * nku + ku] = dr_acc;
+    a.part[nbh * nku + (int64_t)bh * nku + ku] = dw_acc;
   }
 }
 
-// dr[h] = sum_{b,kt} part_r[b,h,kt]; dw likewise.  Block per head, fixed order.
+// dr[h] = sum_{b,u} part_r[b,h,u] over the key units u; dw likewise.  Block per
+// head, fixed order.
 __global__ __launch_bounds__(256) void rw_reduce_kernel(const float* part, float* dr, float* dw, int B, int H,
                                                         int nkt) {
   __shared__ float sr[256], sw[256];
@@ -735,7 +623,7 @@ __global__ __launch_bounds__(256) void rw_reduce_kernel(const float* part, float
 }
 
 // Workspace: [dr/dw partials][dh][1/|q|], each 256-byte aligned.
-static int64_t bwd_part_bytes(const Geometry& g) { return round_up((int64_t)2 * g.B * g.H * g.nkt * 4, 256); }
+static int64_t bwd_part_bytes(const Geometry& g) { return round_up((int64_t)2 * g.B * g.H * 2 * g.nkt * 4, 256); }
 static int64_t bwd_dh_bytes(const Geometry& g) {
   return round_up((int64_t)g.B * g.H * g.Tq_pad * g.DP * (int64_t)g.esize, 256);
 }
@@ -761,18 +649,20 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   ka.eps = c.eps;
   ka.drop = c.drop;
   timer_begin(5, c.stream);
-  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)g.nqt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
+  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3((unsigned)(2 * g.nqt), (unsigned)(g.B * g.H)), dim3(64), 0, c.stream,
+                     ka);
   timer_end(5, c.stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(4, c.stream);
-  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)g.nkt, (unsigned)(g.B * g.H)), dim3(256), 0, c.stream, ka);
+  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)(2 * g.nkt), (unsigned)(g.B * g.H)), dim3(64), 0, c.stream,
+                     ka);
   timer_end(4, c.stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(6, c.stream);
   hipLaunchKernelGGL(rw_reduce_kernel, dim3((unsigned)g.H), dim3(256), 0, c.stream, (const float*)ka.part, c.dr, c.dw,
-                     g.B, g.H, g.nkt);
+                     g.B, g.H, 2 * g.nkt);
   timer_end(6, c.stream);
   return hipGetLastError();
 }

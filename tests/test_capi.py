@@ -42,11 +42,11 @@ def test_version_and_sizes():
     assert L.msa_tile_bits_words(1, 1, 64, 1100) == 2 * 2
     # D=16 is padded to 32 in the workspace
     assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4
-    # backward workspace: (dr, dw) partial per (b, h, key tile), then dh
+    # backward workspace: (dr, dw) partial per (b, h, 32-key unit), then dh
     # (b, h, Tq_pad, DP) in the input type and 1/|q| (b, h, Tq_pad) fp32, each
     # 256-byte aligned
     assert L.msa_bwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == \
-        2 * 4 * 8 * 128 * 4 + 4 * 8 * 8192 * 64 * 2 + 4 * 8 * 8192 * 4
+        2 * 4 * 8 * 256 * 4 + 4 * 8 * 8192 * 64 * 2 + 4 * 8 * 8192 * 4
     assert L.msa_bwd_workspace_bytes(1, 1, 65, 10, 16, 0) == 256 + 128 * 32 * 4 + 512
     assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 48, 0) == 0       # invalid D
     assert L.msa_decode_workspace_bytes(16, 8, 64, 100000) == 16 * 8 * 49 * 64 * 4
