@@ -236,12 +236,12 @@ def main():
 
     nW = window_tiles(T, w) * B
     nU, nA = live_counts(bits, B, H, T)
-    UNIT_FLOP = TILE_FLOP // 4  # one 32x32 unit product with D=64
-    f_total = TILE_FLOP * nW + UNIT_FLOP * nU + 5 * TILE_FLOP * nA
-    # algorithmic flop of each kernel: the screen Q K^T over W (64x64 tiles);
-    # alpha V over the live 32x32 units U; the backward's S recompute, dP, dV,
-    # dK in dkdv and dQ in dq over the live 64x64 tiles A
-    alg_flop = {"fwd_screen_kernel": TILE_FLOP * nW, "fwd_live_kernel": UNIT_FLOP * nU,
+    # canonical algorithmic work on the 64x64 tile grid, C = 2*64*64*D per
+    # tile: fwd+bwd = C (|W| + 6 |A|).  Per kernel: the screen Q K^T over W;
+    # alpha V over A; the backward's S recompute, dP, dV, dK in dkdv and dQ in
+    # dq over A.  (The kernels themselves visit only the live 32x32 units, nU.)
+    f_total = TILE_FLOP * (nW + 6 * nA)
+    alg_flop = {"fwd_screen_kernel": TILE_FLOP * nW, "fwd_live_kernel": TILE_FLOP * nA,
                 "dkdv_kernel": TILE_FLOP * 4 * nA, "dq_kernel": TILE_FLOP * nA}
     dom_flop = alg_flop.get(dom)
     achieved = dom_flop / (dom_ms * 1e-3) / 1e12 if dom_flop else None

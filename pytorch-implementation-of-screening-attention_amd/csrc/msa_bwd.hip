@@ -275,6 +275,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
 
   for (;;) {
     const int k0 = cur * kUnit;
+    // the next unit's rows load while this one is computed (past the last
+    // unit, the current one again, a cache hit: every iteration then waits
+    // for the same count)
+    const int nxt = walk.next();
+    const int nl = nxt >= 0 ? nxt : cur;
+    frag kn[NKS], vn[NKS];
+    load_rows(kb0, a.ks.st, nl, kn);
+    load_rows(vb0, a.vs.st, nl, vn);
+    const bool kokn = key_ok(nl);
     zero_tail(kc);
     zero_tail(vc);
     // register r -> key k0 + rowof(r, half), lane -> query i
@@ -293,7 +302,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
       s2v = frag_dot(vc[ks], vc[ks], s2v);
     }
     guard_frags(vc);
-    const int nxt = walk.next();
     s2k += __shfl_xor(s2k, 32);
     s2v += __shfl_xor(s2v, 32);
     {
@@ -316,19 +324,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     // a conservative gate on the products (s > thr |q|), then the exact
     // test only for registers where some lane passes
     const int rel0 = i - (k0 + 8 * half);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float ds = 0.0f;
-      if (__ballot(s[r] > thq) != 0ull) {
+    {
+      const uint32_t pm0 = pass_mask(s, thq);
+      for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
         const int dd = rel0 - (16 * (r >> 3) + (r & 7));
         const float av = trim(s[r] * iql, hp.r);
+        float ds = 0.0f;
         if (av > 0.0f && valid && in_window(dd, hp)) {
           ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r];
           if (a.drop.on) ds *= dropout_factor(a.drop, bh, i, i - dd);
         }
-      }
-      dp[r] = ds;
-      __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
+        dp[r] = ds;
+      });
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (((pm0 >> r) & 1u) == 0u) dp[r] = 0.0f;
     }
     // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
     // the key rows, one 32-column block of d at a time
@@ -359,9 +369,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     guard_frags(db);
     if (nxt < 0) break;
     cur = nxt;
-    load_rows(kb0, a.ks.st, cur, kc);
-    load_rows(vb0, a.vs.st, cur, vc);
-    kok = key_ok(cur);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      kc[ks] = kn[ks];
+      vc[ks] = vn[ks];
+    }
+    kok = kokn;
   }
   guard_frags(qb);
   guard_frags(hb);
@@ -517,13 +530,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     // a conservative gate on the products (s > thr |k|), then the exact
     // test only for registers where some lane passes
     const int rel0 = (q0 + 8 * half) - j;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float p = 0.0f, ds = 0.0f;
-      if (__ballot(s[r] > thk) != 0ull) {
+    {
+      const uint32_t pm0 = pass_mask(s, thk);
+      for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
         const int dd = rel0 + 16 * (r >> 3) + (r & 7);
         const float sv = s[r] * ikl;
         const float av = trim(sv, hp.r);
+        float p = 0.0f, ds = 0.0f;
         if (av > 0.0f && in_window(dd, hp)) {
           const float c = a.drop.on ? dropout_factor(a.drop, bh, j + dd, j) : 1.0f;
           const float mk = softmask(dd, hp.iw) * c;
@@ -533,10 +546,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
           dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
           dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
         }
-      }
-      s[r] = p;
-      dp[r] = ds;
-      __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
+        s[r] = p;
+        dp[r] = ds;
+      });
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (((pm0 >> r) & 1u) == 0u) { s[r] = 0.0f; dp[r] = 0.0f; }
     }
     {
       float sc[16];

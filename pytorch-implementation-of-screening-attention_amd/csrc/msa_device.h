@@ -222,6 +222,34 @@ __device__ inline HeadParams head_params(const float* r, const float* w, int h, 
   return p;
 }
 
+// Wave-uniform mask of the registers r of a C block for which some lane has
+// c[r] > th.
+__device__ inline uint32_t pass_mask(const f32x16& c, float th) {
+  uint32_t m = 0u;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) m |= __ballot(c[r] > th) != 0ull ? (1u << r) : 0u;
+  return m;
+}
+// Calls fn(r) for each register r whose bit is set in the uniform mask pm.
+// Indexed form: a loop over the set bits only, r uniform, so c[r] inside fn
+// is a register-indexed move (s_set_gpr_idx), not a memory access.  Unrolled
+// form: a compile-time r and one uniform branch per register.  The fp32
+// kernels, whose register files are full (accumulators partly in AGPRs), use
+// the unrolled form: with the indexed one their dK parity test failed, and
+// the cause is not established.
+template <bool kIndexed, typename Fn>
+__device__ inline void for_each_set(uint32_t pm, Fn&& fn) {
+  if constexpr (kIndexed) {
+    for (; pm != 0u; pm &= pm - 1u) fn(__builtin_ctz(pm));
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if ((pm >> r) & 1u) fn(r);
+      __builtin_amdgcn_sched_barrier(0);  // one register at a time: few live temporaries
+    }
+  }
+}
+
 // Branch-free in-window test on the integer distance dd = i - j.
 __device__ inline bool in_window(int dd, const HeadParams& hp) { return (unsigned)(dd + hp.wsh) < hp.wlim; }
 

@@ -569,18 +569,21 @@ void fwd_live_kernel(FwdKArgs a) {
     // P^T[j][i] = alpha_ij m_ij / |v_j|: a conservative gate on the raw
     // products (s > thr), the exact test only where some lane passes
     const int rel0 = i - (k0 + 8 * half);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float p = 0.0f;
-      if (__ballot(s[r] > thq) != 0ull) {
+    {
+      const uint32_t pm0 = pass_mask(s, thq);
+      for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
         const int dd = rel0 - (16 * (r >> 3) + (r & 7));
         const float av = trim(s[r] * iq, hp.r);
+        float p = 0.0f;
         if (av > 0.0f && in_window(dd, hp)) {
           p = av * av * softmask(dd, hp.iw) * sv[rowof(r, half)];
           if (a.drop.on) p *= dropout_factor(a.drop, bh, i, i - dd);
         }
-      }
-      s[r] = p;
+        s[r] = p;
+      });
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (((pm0 >> r) & 1u) == 0u) s[r] = 0.0f;
     }
     // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
     frag pb[NC];
