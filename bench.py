@@ -31,7 +31,7 @@ PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 TILE_FLOP = 2 * 64 * 64 * 64  # one 64x64 tile product with D=64
 KERNELS = {1: "prep_k_kernel", 2: "fwd_screen_kernel", 3: "fwd_live_kernel", 4: "dkdv_kernel",
-           5: "dq_kernel", 6: "rw_reduce_kernel"}   # msa_kernel_id values (include/msa.h)
+           5: "dq_kernel"}   # msa_kernel_id values (include/msa.h)
 
 
 def parse():

@@ -166,7 +166,7 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
  * for concurrent use from several threads. */
 enum msa_kernel_id {
   MSA_K_PREP_K = 1, MSA_K_FWD_SCREEN = 2, MSA_K_FWD_LIVE = 3, MSA_K_DKDV = 4,
-  MSA_K_DQ = 5, MSA_K_RW_REDUCE = 6, MSA_K_DECODE = 7
+  MSA_K_DQ = 5, /* 6: unused (no separate dr/dw reduction launch) */ MSA_K_DECODE = 7
 };
 int msa_timer_arm(int kernel, int n);
 int msa_timer_read(int kernel, float* ms, int n);

@@ -22,12 +22,13 @@
 // (attention.py:185-188) enters as a zero 1/|k|, which gives s = 0 and so
 // alpha = 0 for those keys.
 //
-//   dq_kernel       : wave per 32-query unit over its live key units; also
-//                     leaves dh and 1/|q| of those rows for dkdv_kernel.
-//   dkdv_kernel     : wave per 32-key unit; accumulates dv^, dk^ in MFMA
-//                     registers over its live query units, writes dk, dv and
-//                     one (dr, dw) partial.
-//   rw_reduce_kernel: fixed-order sum of the partials -> dr, dw.
+//   dq_kernel   : wave per 32-query unit over its live key units; writes dq
+//                 and the unit's (dr, dw) share, and leaves dh and 1/|q| of
+//                 its rows for dkdv_kernel.
+//   dkdv_kernel : wave per 32-key unit; accumulates dv^, dk^ in MFMA
+//                 registers over its live query units and writes dk, dv; one
+//                 wave per head also sums the (dr, dw) shares in a fixed
+//                 order into dr, dw.
 // No atomics anywhere, so every gradient is bitwise reproducible.
 #include "msa_device.h"
 #include "msa_internal.h"
@@ -64,7 +65,8 @@ struct BwdKArgs {
   const void* y; const void* dy; const float* hnorm;
   const float* r; const float* w;
   const uint32_t* bits;
-  void* dq; void* dk; void* dv; float* part;
+  void* dq; void* dk; void* dv; float* dr; float* dw;
+  float* part;  // workspace: (dr, dw) shares per (b, h, query unit), [2][b*h][2*nqt]
   void* dh; float* iqs;  // workspace: dh [b*h][Tq_pad][DP] (T), 1/|q| [b*h][Tq_pad]
   int B, H, Tq, Tk, D, nqt, nkt, nku_words, causal;
   int64_t Tq_pad;
@@ -201,7 +203,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   auto bitf = [brow](int u) { return ((brow[u >> 5] >> (u & 31)) & 1u) != 0u; };
   BitWalk<decltype(bitf)> walk(bitf, ku_lo, ku_hi);
   int cur = walk.next();
-  if (cur < 0) {  // wave-uniform: no live key unit, dq = 0
+  const int64_t nbh = (int64_t)a.B * a.H;
+  const int nqu = 2 * a.nqt;
+  if (cur < 0) {  // wave-uniform: no live key unit, dq = 0 and no share of dr, dw
     if (valid)
 #pragma unroll
       for (int dblk = 0; dblk < NDH; ++dblk)
@@ -210,6 +214,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
           const int d = 32 * dblk + 8 * g + 4 * half;
           if (d < a.D) store4(dqrow + d, 0.0f, 0.0f, 0.0f, 0.0f);
         }
+    if (lane == 0) {
+      a.part[(int64_t)bh * nqu + qu] = 0.0f;
+      a.part[nbh * nqu + (int64_t)bh * nqu + qu] = 0.0f;
+    }
     return;
   }
 
@@ -267,6 +275,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     if (half == 0) a.iqs[(int64_t)bh * a.Tq_pad + i] = valid ? iql : 0.0f;
   }
   const float thq = hp.thr / iql;  // s > thr  <=>  (q . k)/|k| > thr |q|
+  float dr_acc = 0.0f, dw_acc = 0.0f;  // this unit's share of dr, dw
   f32x16 adq[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
@@ -328,11 +337,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
       const uint32_t pm0 = pass_mask(s, thq);
       for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
         const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-        const float av = trim(s[r] * iql, hp.r);
+        const float sv = s[r] * iql;
+        const float av = trim(sv, hp.r);
         float ds = 0.0f;
         if (av > 0.0f && valid && in_window(dd, hp)) {
-          ds = 2.0f * av * hp.r * softmask(dd, hp.iw) * dp[r];
-          if (a.drop.on) ds *= dropout_factor(a.drop, bh, i, i - dd);
+          const float c = a.drop.on ? dropout_factor(a.drop, bh, i, i - dd) : 1.0f;
+          const float mk = softmask(dd, hp.iw) * c;
+          const float g = dp[r];
+          ds = 2.0f * av * hp.r * mk * g;
+          dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
+          dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
         }
         dp[r] = ds;
       });
@@ -379,6 +393,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   guard_frags(qb);
   guard_frags(hb);
   write_norm_bwd<T, DP>(adq, qb, valid, a.D, a.eps, half, dqrow);
+  dr_acc = wave_sum(dr_acc);
+  dw_acc = wave_sum(dw_acc);
+  if (lane == 0) {
+    a.part[(int64_t)bh * nqu + qu] = dr_acc;
+    a.part[nbh * nqu + (int64_t)bh * nqu + qu] = dw_acc;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -413,8 +433,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   const bool jvalid = j < a.Tk;
   const int jj = jvalid ? j : 0;
   const int64_t orow = (((int64_t)b * a.Tk + jj) * a.H + h) * a.D;
-  const int64_t nbh = (int64_t)a.B * a.H;
-  const int nku = 2 * a.nkt;
+  if (ku == 2 * a.nkt - 1 && bh < a.H) {
+    // one wave per head: dr, dw from dq_kernel's per-query-unit shares
+    // (complete: dq_kernel ran first), summed in a fixed order
+    const int64_t nbh = (int64_t)a.B * a.H;
+    const int nqu = 2 * a.nqt;
+    float ar = 0.0f, aw = 0.0f;
+    for (int64_t idx = lane; idx < (int64_t)a.B * nqu; idx += kWave) {
+      const int bb = (int)(idx / nqu), u = (int)(idx % nqu);
+      const int64_t o = ((int64_t)bb * a.H + bh) * nqu + u;
+      ar += a.part[o];
+      aw += a.part[nbh * nqu + o];
+    }
+    ar = wave_sum(ar);
+    aw = wave_sum(aw);
+    if (lane == 0) {
+      a.dr[bh] = ar;
+      a.dw[bh] = aw;
+    }
+  }
 
   int qu_lo, qu_hi;
   {
@@ -443,10 +480,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
             store4((T*)a.dv + orow + d, 0.0f, 0.0f, 0.0f, 0.0f);
           }
         }
-    if (lane == 0) {
-      a.part[(int64_t)bh * nku + ku] = 0.0f;
-      a.part[nbh * nku + (int64_t)bh * nku + ku] = 0.0f;
-    }
     return;
   }
 
@@ -499,7 +532,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) { acc_k[dblk][r] = 0.0f; acc_v[dblk][r] = 0.0f; }
-  float dr_acc = 0.0f, dw_acc = 0.0f;
   const float thk = hp.thr / ikl;  // s > thr  <=>  (q . k)/|q| > thr |k|  (+inf for masked keys)
 
   for (;;) {
@@ -543,8 +575,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
           const float g = dp[r];
           p = av * av * mk;
           ds = 2.0f * av * hp.r * mk * g;
-          dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
-          dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
         }
         s[r] = p;
         dp[r] = ds;
@@ -602,43 +632,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
 
   write_norm_bwd<T, DP>(acc_k, kb, jvalid, a.D, a.eps, half, (T*)a.dk + orow);
   write_norm_bwd<T, DP>(acc_v, vb, jvalid, a.D, a.eps, half, (T*)a.dv + orow);
-  dr_acc = wave_sum(dr_acc);
-  dw_acc = wave_sum(dw_acc);
-  if (lane == 0) {
-    a.part[(int64_t)bh * nku + ku] = dr_acc;
-    a.part[nbh * nku + (int64_t)bh * nku + ku] = dw_acc;
-  }
-}
-
-// dr[h] = sum_{b,u} part_r[b,h,u] over the key units u; dw likewise.  Block per
-// head, fixed order.
-__global__ __launch_bounds__(256) void rw_reduce_kernel(const float* part, float* dr, float* dw, int B, int H,
-                                                        int nkt) {
-  __shared__ float sr[256], sw[256];
-  const int h = blockIdx.x;
-  const int64_t nbh = (int64_t)B * H;
-  float ar = 0.0f, aw = 0.0f;
-  for (int64_t idx = threadIdx.x; idx < (int64_t)B * nkt; idx += 256) {
-    const int b = (int)(idx / nkt), kt = (int)(idx % nkt);
-    const int64_t o = ((int64_t)b * H + h) * nkt + kt;
-    ar += part[o];
-    aw += part[nbh * nkt + o];
-  }
-  sr[threadIdx.x] = ar;
-  sw[threadIdx.x] = aw;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      sr[threadIdx.x] += sr[threadIdx.x + s];
-      sw[threadIdx.x] += sw[threadIdx.x + s];
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) { dr[h] = sr[0]; dw[h] = sw[0]; }
 }
 
 // Workspace: [dr/dw partials][dh][1/|q|], each 256-byte aligned.
-static int64_t bwd_part_bytes(const Geometry& g) { return round_up((int64_t)2 * g.B * g.H * 2 * g.nkt * 4, 256); }
+static int64_t bwd_part_bytes(const Geometry& g) { return round_up((int64_t)2 * g.B * g.H * 2 * g.nqt * 4, 256); }
 static int64_t bwd_dh_bytes(const Geometry& g) {
   return round_up((int64_t)g.B * g.H * g.Tq_pad * g.DP * (int64_t)g.esize, 256);
 }
@@ -653,7 +650,7 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   ka.q = c.q; ka.qs = c.qs; ka.k = c.k; ka.ks = c.ks; ka.v = c.v; ka.vs = c.vs; ka.kpm = c.kpm;
   ka.y = c.y; ka.dy = c.dy; ka.hnorm = c.hnorm;
   ka.r = c.r; ka.w = c.w; ka.bits = c.bits;
-  ka.dq = c.dq; ka.dk = c.dk; ka.dv = c.dv;
+  ka.dq = c.dq; ka.dk = c.dk; ka.dv = c.dv; ka.dr = c.dr; ka.dw = c.dw;
   char* ws = (char*)c.workspace;
   ka.part = (float*)ws;
   ka.dh = ws + bwd_part_bytes(g);
@@ -673,12 +670,6 @@ static hipError_t launch_bwd_t(const BwdCall& c) {
   hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3((unsigned)(2 * g.nkt), (unsigned)(g.B * g.H)), dim3(64), 0, c.stream,
                      ka);
   timer_end(4, c.stream);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  timer_begin(6, c.stream);
-  hipLaunchKernelGGL(rw_reduce_kernel, dim3((unsigned)g.H), dim3(256), 0, c.stream, (const float*)ka.part, c.dr, c.dw,
-                     g.B, g.H, 2 * g.nkt);
-  timer_end(6, c.stream);
   return hipGetLastError();
 }
 

@@ -14,7 +14,7 @@ MSA_F32 = 0
 MSA_BF16 = 1
 
 # kernel ids for msa_timer_arm (include/msa.h)
-K_PREP_K, K_FWD_SCREEN, K_FWD_LIVE, K_DKDV, K_DQ, K_RW_REDUCE, K_DECODE = 1, 2, 3, 4, 5, 6, 7
+K_PREP_K, K_FWD_SCREEN, K_FWD_LIVE, K_DKDV, K_DQ, K_DECODE = 1, 2, 3, 4, 5, 7
 
 _lock = threading.Lock()
 _lib = None
