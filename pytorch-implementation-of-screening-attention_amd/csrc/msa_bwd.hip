@@ -419,6 +419,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   __shared__ __attribute__((aligned(16))) float sq[32];  // 1/|q| of the current query unit's rows
+  __shared__ typename Mma<T>::frag kvs[2 * (DP / Mma<T>::KS)][kWave];  // own raw k, v operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int ku, bh;
   xcd_interleave(ku, bh);
@@ -512,9 +513,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     }
   };
 
-  // own keys as raw B operands (lane -> key) with 1/|k| (0 if padded or
-  // masked) and 1/|v|; their loads go first, the first query unit's behind
-  frag kb[NKS], vb[NKS], qf[NKS], hf[NKS];
+  // own keys as raw B operands (lane -> key), kept in LDS (read back per
+  // query unit; the registers hold the next unit's rows instead), with 1/|k|
+  // (0 if padded or masked) and 1/|v|; their loads go first, the first query
+  // unit's behind
+  frag qf[NKS], hf[NKS];
   float ikl, ivl, iqv;
   {
     KeyRows<T, DP> kr;
@@ -523,8 +526,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     kr.finish(a.eps, ikl, ivl);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      kb[ks] = kr.k.f[ks];
-      vb[ks] = kr.v.f[ks];
+      kvs[ks][lane] = kr.k.f[ks];
+      kvs[NKS + ks][lane] = kr.v.f[ks];
     }
   }
   f32x16 acc_k[NDH], acc_v[NDH];
@@ -536,6 +539,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
 
   for (;;) {
     const int q0 = cur * kUnit;
+    // the next unit's rows load while this one is computed (past the last
+    // unit, the current one again, a cache hit: every iteration then waits
+    // for the same count)
+    const int nxt = walk.next();
+    frag qn[NKS], hn[NKS];
+    float iqn;
+    load_unit(nxt >= 0 ? nxt : cur, qn, hn, iqn);
     zero_tail(qf);
     wave_lds_sync();
     if (half == 0) sq[l32] = iqv;
@@ -545,11 +555,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     f32x16 s, dp;
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
+    {
+      frag g[NKS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(qf[ks], kb[ks], s);
+      for (int ks = 0; ks < NKS; ++ks) g[ks] = kvs[ks][lane];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) dp = M::mma_ng(hf[ks], vb[ks], dp);
-    const int nxt = walk.next();
+      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(qf[ks], g[ks], s);
+      guard_frags(g);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) g[ks] = kvs[NKS + ks][lane];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) dp = M::mma_ng(hf[ks], g[ks], dp);
+      guard_frags(g);
+    }
     {
       float sc[16];
       read_row_scales(sq, half, sc);
@@ -625,13 +643,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     guard_frags(db);
     if (nxt < 0) break;
     cur = nxt;
-    load_unit(cur, qf, hf, iqv);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      qf[ks] = qn[ks];
+      hf[ks] = hn[ks];
+    }
+    iqv = iqn;
   }
-  guard_frags(kb);
-  guard_frags(vb);
 
-  write_norm_bwd<T, DP>(acc_k, kb, jvalid, a.D, a.eps, half, (T*)a.dk + orow);
-  write_norm_bwd<T, DP>(acc_v, vb, jvalid, a.D, a.eps, half, (T*)a.dv + orow);
+  {
+    frag x[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) x[ks] = kvs[ks][lane];
+    write_norm_bwd<T, DP>(acc_k, x, jvalid, a.D, a.eps, half, (T*)a.dk + orow);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) x[ks] = kvs[NKS + ks][lane];
+    write_norm_bwd<T, DP>(acc_v, x, jvalid, a.D, a.eps, half, (T*)a.dv + orow);
+  }
 }
 
 // Workspace: [dr/dw partials][dh][1/|q|], each 256-byte aligned.
