@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--calib-copy", action="store_true",
-                   help="end with a plain 256 MiB device copy (rocprofv3 --pmc byte-counter calibration)")
+                   help="end with one elementwise pass over 2 GiB (rocprofv3 --pmc byte-counter calibration)")
     return p.parse_args()
 
 
@@ -285,12 +285,14 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, H, D, r, w, args.seed)
     if args.calib_copy:
-        src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+        # one elementwise pass of known traffic (reads and writes 2 GiB of fp32,
+        # well past the 256 MB last-level cache), for scaling the byte counters
+        src = torch.ones(512 << 20, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        out["calib_copy_bytes"] = src.numel() * 2
+        out["calib_copy_bytes"] = src.numel() * 4
     print(json.dumps(out), flush=True)
 
 
