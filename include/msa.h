@@ -179,11 +179,6 @@ int msa_selftest_mfma(const float* a16, const float* b16, float* out16,
                       const float* a2, const float* b2, float* out2,
                       void* stream);
 
-/* Device self-test of the int8 MFMA layout the forward's pre-screen assumes:
- * out (32x32 int32, row-major) = a (32x32 int8) . b (32x32 int8), both
- * row-major.  Test infrastructure only. */
-int msa_selftest_mfma_i8(const int8_t* a, const int8_t* b, int32_t* out, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

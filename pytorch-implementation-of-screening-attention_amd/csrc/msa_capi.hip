@@ -327,9 +327,4 @@ int msa_selftest_mfma(const float* a16, const float* b16, float* out16, const fl
   return hip_status(msa::launch_selftest(a16, b16, out16, a2, b2, out2, (hipStream_t)stream), "selftest launch");
 }
 
-int msa_selftest_mfma_i8(const int8_t* a, const int8_t* b, int32_t* out, void* stream) {
-  if (a == nullptr || b == nullptr || out == nullptr) return fail(MSA_ERR_INVALID, "selftest buffers are null");
-  return hip_status(msa::launch_selftest_i8(a, b, out, (hipStream_t)stream), "selftest launch");
-}
-
 }  // extern "C"

@@ -232,26 +232,4 @@ hipError_t launch_selftest(const float* a16, const float* b16, float* out16, con
   return hipGetLastError();
 }
 
-// The int8 form (v_mfma_i32_32x32x32_i8): lane l supplies row/column l%32
-// and 16 contraction values of slot group l/32; the i32 result has the fp32
-// 32x32 C layout.
-__global__ __launch_bounds__(64) void selftest_i8_kernel(const int8_t* a, const int8_t* b, int32_t* out) {
-  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
-  i8x16 fa, fb;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    fa[e] = a[l32 * 32 + 16 * half + e];      // A[m=l32][k]
-    fb[e] = b[(16 * half + e) * 32 + l32];    // B[k][n=l32]
-  }
-  i32x16 c = {};
-  c = mma_i8(fa, fb, c);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) out[(8 * (r / 4) + 4 * half + (r % 4)) * 32 + l32] = c[r];
-}
-
-hipError_t launch_selftest_i8(const int8_t* a, const int8_t* b, int32_t* out, hipStream_t stream) {
-  hipLaunchKernelGGL(selftest_i8_kernel, dim3(1), dim3(64), 0, stream, a, b, out);
-  return hipGetLastError();
-}
-
 }  // namespace msa

@@ -13,8 +13,6 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
-typedef __attribute__((__vector_size__(16 * sizeof(int8_t)))) int8_t i8x16;
-typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16;
 
 constexpr int kWave = 64;
 constexpr int kTile = 64;  // rows of a query tile and of a key tile
@@ -121,17 +119,6 @@ template <> struct Mma<float> {
   __device__ static inline float get(const frag& f, int) { return f; }
   __device__ static inline frag pack(const f32x16& c, int r0) { return c[r0]; }
 };
-
-// int8 product 32x32x32 (v_mfma_i32_32x32x32_i8): lane l supplies row (A) /
-// column (B) l%32 and 16 contraction values of slot group l/32; the i32
-// result has the C layout above.  Exact (integer) accumulation.
-typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
-__device__ inline i32x16 mma_i8(i8x16 a, i8x16 b, i32x16 c) {
-  i32x4 av = __builtin_bit_cast(i32x4, a), bv = __builtin_bit_cast(i32x4, b);
-  const i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, c, 0, 0, 0);
-  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(av), "+v"(bv));
-  return d;
-}
 
 // Row permutation applied when a lane loads row (l%32) of an A operand whose
 // product lands in a C block that is later consumed as the B operand of a

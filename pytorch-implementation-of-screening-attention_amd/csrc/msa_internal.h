@@ -105,6 +105,5 @@ void timer_end(int kernel, hipStream_t s);
 hipError_t launch_selftest(const float* a16, const float* b16, float* out16,
                            const float* a2, const float* b2, float* out2,
                            hipStream_t stream);
-hipError_t launch_selftest_i8(const int8_t* a, const int8_t* b, int32_t* out, hipStream_t stream);
 
 }  // namespace msa

@@ -45,7 +45,6 @@ _SIGS = {
     "msa_timer_arm": (_i, [_i, _i]),
     "msa_timer_read": (_i, [_i, ctypes.POINTER(ctypes.c_float), _i]),
     "msa_selftest_mfma": (_i, [_p, _p, _p, _p, _p, _p, _p]),
-    "msa_selftest_mfma_i8": (_i, [_p, _p, _p, _p]),
 }
 
 EXPORTED = tuple(_SIGS)

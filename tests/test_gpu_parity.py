@@ -61,22 +61,6 @@ def test_mfma_layout_selftest():
                                rtol=1e-6, atol=1e-5)
 
 
-def test_mfma_i8_layout_selftest():
-    # the int8 pre-screen's operand and result maps: exact integer product
-    from multiscreen import _native
-    L = _native.lib()
-    g = torch.Generator().manual_seed(1)
-    a = torch.randint(-127, 128, (32, 32), generator=g, dtype=torch.int8)
-    b = torch.randint(-127, 128, (32, 32), generator=g, dtype=torch.int8)
-    out = torch.zeros(32, 32, dtype=torch.int32, device=DEV)
-    ta, tb = a.to(DEV).contiguous(), b.to(DEV).contiguous()
-    rc = L.msa_selftest_mfma_i8(ta.data_ptr(), tb.data_ptr(), out.data_ptr(), torch.cuda.current_stream().cuda_stream)
-    assert rc == 0
-    torch.cuda.synchronize()
-    want = a.long() @ b.long()
-    assert torch.equal(out.cpu().long(), want)
-
-
 FWD_CASES = [
     # B, Tq, Tk, H, D, causal, r, w, kpm
     (2, 128, 128, 8, 64, True, [1.1] * 8, [16, 32, 64, 96, 128, 160, 200, 256], False),
