@@ -241,6 +241,52 @@ def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
     assert np.array_equal(got.reshape(B, H, nqu // 2, 2, nku // 2, 2).any(axis=(3, 5)), act64)
 
 
+def _bf16_unit_bits(q, k, r, w, causal):
+    """Live 32x32 units of the bf16 screen's exact test, restated in float64:
+    s = (q . k^)/|q| with k^ = bf16(k/|k|) as the forward stores it, and the
+    distance of each unit's best in-window pair from the threshold."""
+    qn = np64(q) / np.maximum(np.linalg.norm(np64(q), axis=-1, keepdims=True), 1e-8)
+    kf = k.float()
+    kh = (kf / kf.norm(dim=-1, keepdim=True).clamp_min(1e-8)).bfloat16().double().numpy()
+    B, T, H, _ = qn.shape
+    n = T // 32
+    live = np.zeros((B, H, n, n), dtype=bool)
+    margin = np.full((B, H, n, n), np.inf)
+    i = np.arange(T)[:, None]
+    j = np.arange(T)[None, :]
+    for h in range(H):
+        s = np.einsum("bid,bjd->bij", qn[:, :, h], kh[:, :, h])
+        wc = math.ceil(w[h])
+        inside = ((i - j >= 0) & (i - j < wc)) if causal else (np.abs(i - j) < wc)
+        thr = 1.0 - 1.0 / r[h]
+        d = np.where(inside[None], s - thr, -np.inf).reshape(B, n, 32, n, 32)
+        best = d.max(axis=(2, 4))
+        live[:, h] = best > 0
+        margin[:, h] = np.abs(best)
+    return live, margin
+
+
+@pytest.mark.parametrize("r", [1.9, 2.0, 2.1, 1.5])
+def test_bf16_bitmap_matches_exact_test(r):
+    # the bf16 screen's bitmap is the exact test on its own operands (bf16 K^,
+    # raw q scaled by 1/|q|), restated in float64; units within 1e-5 of the
+    # threshold excepted
+    B, T, H, D = 2, 1024, 4, 64
+    q, k, v = qkv(B, T, T, H, D, seed=11, dtype=torch.bfloat16)
+    rr, ww = [r] * H, [100.0, 400.0, 700.0, 1e5]
+    y, hnorm, bits = _run_fwd(q, k, v, rr, ww, True)
+    want, margin = _bf16_unit_bits(q, k, rr, ww, True)
+    n = T // 32
+    words = (n + 31) // 32
+    b = bits.cpu().numpy().view(np.uint32).reshape(B, H, n, words)
+    got = np.zeros((B, H, n, n), dtype=bool)
+    for ku in range(n):
+        got[..., ku] = (b[..., ku // 32] >> (ku % 32)) & 1
+    assert want.sum() > 0
+    diff = got != want
+    assert np.all(margin[diff] < 1e-5), (int(diff.sum()), float(margin[diff].min()) if diff.any() else 0.0)
+
+
 def test_window_and_threshold_skip_are_exact():
     # keys outside every query's window, or below threshold, must not change y at all
     B, T, H, D = 1, 512, 2, 64
