@@ -8,6 +8,8 @@
 // and reads a V row only when its alpha*m is non-zero.  Because screening has
 // no softmax normaliser (attention.py:192-193), chunk partials simply add; a
 // second kernel sums them in a fixed order and applies TanhNorm (norm.py:23-25).
+#include <type_traits>
+
 #include "msa_device.h"
 #include "msa_internal.h"
 
@@ -43,6 +45,24 @@ template <> struct Vec16<float> {
   }
   __device__ static inline float get(const type& a, int e) { return a[e]; }
 };
+
+// Sum over aligned groups of G lanes (G a power of two <= 64), every lane of
+// a group getting the group's total: DPP lane swaps within rows of 16 (xor 1,
+// xor 2, then the 8- and 16-lane mirrors, which pair each half with the other
+// once both halves hold their own sums), lane shuffles beyond.
+template <int G>
+__device__ inline float group_sum(float x) {
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (G >= 2) x += dpp(x, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) x += dpp(x, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) x += dpp(x, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (G >= 16) x += dpp(x, std::integral_constant<int, 0x140>{}); // row_mirror
+#pragma unroll
+  for (int o = 16; o < G; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
@@ -88,20 +108,17 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
       }
 #pragma unroll
       for (int u = 0; u < kDecUnroll; ++u) {
-        float dot = V::dot(qv, kv[u], 0.0f), ss = V::dot(kv[u], kv[u], 0.0f);
-#pragma unroll
-        for (int o = 1; o < LPK; o <<= 1) { dot += __shfl_xor(dot, o); ss += __shfl_xor(ss, o); }
-        const float s = dot * iq * (1.0f / fmaxf(sqrtf(ss), a.eps));
+        const float dot = group_sum<LPK>(V::dot(qv, kv[u], 0.0f));
+        const float ss = group_sum<LPK>(V::dot(kv[u], kv[u], 0.0f));
+        const float s = dot * iq * inv_len(ss, a.eps);
         const float av = trim(s, hp.r);
         const int64_t j = base + u * KPW + kl;
         if (j < cend && av > 0.0f) {
           // every lane of the key's group takes this branch together
           const float m = softmask((int)(pos - j), hp.iw);
           const vec vv = *reinterpret_cast<const vec*>(vb + j * a.vs.st);
-          float vs2 = V::dot(vv, vv, 0.0f);
-#pragma unroll
-          for (int o = 1; o < LPK; o <<= 1) vs2 += __shfl_xor(vs2, o);
-          const float coef = av * av * m / fmaxf(sqrtf(vs2), a.eps);
+          const float vs2 = group_sum<LPK>(V::dot(vv, vv, 0.0f));
+          const float coef = av * av * m * inv_len(vs2, a.eps);
 #pragma unroll
           for (int e = 0; e < VEC; ++e) acc[e] += coef * V::get(vv, e);
         }
