@@ -135,7 +135,7 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[DP / 32], const typena
   float ss = 0.0f;
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) ss = frag_dot(x[ks], x[ks], ss);
-  ss += __shfl_xor(ss, 32);
+  ss = half_sum(ss);
   const float nx = sqrtf(ss);
   const float ix = 1.0f / fmaxf(nx, eps);
   float dot = 0.0f;
@@ -143,7 +143,7 @@ __device__ inline void write_norm_bwd(const f32x16 (&acc)[DP / 32], const typena
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dot += M::get(x[creg_ks<T>(dblk, r)], creg_e<T>(r)) * ix * acc[dblk][r];
-  dot += __shfl_xor(dot, 32);
+  dot = half_sum(dot);
   const float proj = nx > eps ? dot : 0.0f;
   if (!valid) return;
   store_creg_row<T, NDH>(out, D, half, [&](int dblk, int r) {
@@ -311,8 +311,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
       s2v = frag_dot(vc[ks], vc[ks], s2v);
     }
     guard_frags(vc);
-    s2k += __shfl_xor(s2k, 32);
-    s2v += __shfl_xor(s2v, 32);
+    s2k = half_sum(s2k);
+    s2v = half_sum(s2v);
     {
       const float ik = kok ? inv_len(s2k, a.eps) : 0.0f;
       const float iv = inv_len(s2v, a.eps);

@@ -269,6 +269,15 @@ __device__ inline float softmask_dw(int dd, float iw) {
   return 0.5f * sinpif(x) * 3.14159265358979f * rel * iw * iw;
 }
 
+// x[l] + x[l ^ 32] in every lane, with one v_permlane32_swap (no LDS): the
+// swap leaves lanes 0..31 of the first result and 32..63 of the second with
+// the lane's own value and the others with the partner's, so the two results
+// add to the pair sum in every lane.
+__device__ inline float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -391,7 +400,7 @@ struct PRow {
     float s = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) s = frag_dot(f[ks], o.f[ks], s);
-    return s + __shfl_xor(s, 32);
+    return half_sum(s);
   }
   __device__ inline float inv_norm(float eps) const { return inv_len(dot(*this), eps); }
   // this <- a*this + b*o, rounded to T

@@ -543,7 +543,7 @@ void fwd_live_kernel(FwdKArgs a) {
       float s2 = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) s2 = frag_dot(vc[ks], vc[ks], s2);
-      s2 += __shfl_xor(s2, 32);
+      s2 = half_sum(s2);
       const float iv = inv_len(s2, a.eps);
       wave_lds_sync();
       if (half == 0) sv[m] = iv;
@@ -606,7 +606,7 @@ void fwd_live_kernel(FwdKArgs a) {
   for (int dblk = 0; dblk < NDH; ++dblk)
 #pragma unroll
     for (int r = 0; r < 16; ++r) ss += o[dblk][r] * o[dblk][r];
-  ss += __shfl_xor(ss, 32);
+  ss = half_sum(ss);
   const float n = sqrtf(ss);
   const float nc = fmaxf(n, a.eps);
   const float f = tanhf(nc) / nc;
