@@ -172,12 +172,13 @@ constexpr int bwd_waves() { return sizeof(T) == 2 && DP <= 64 ? 2 : 1; }
 // dkdv_kernel reads).
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T, DP>()))) void dq_kernel(BwdKArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1))) void dq_kernel(BwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k| (0 if padded or masked) of the unit's key rows
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v|
+  __shared__ typename Mma<T>::frag qh[2 * (DP / Mma<T>::KS)][kWave];  // own raw q, dh operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
   xcd_interleave(qu, bh);
@@ -251,8 +252,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     return j < a.Tk && !(a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + j] != 0);
   };
 
-  // own queries' rows first, then the first key unit's rows behind them
-  frag qb[NKS], hb[NKS], kc[NKS], vc[NKS];
+  // own queries' rows first, then the first key unit's rows behind them;
+  // the raw q and dh operand fragments are kept in LDS (read back per key
+  // unit), which leaves registers for three waves per SIMD
+  frag kc[NKS], vc[NKS];
   float iql;
   bool kok;
   {
@@ -262,16 +265,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     load_rows(vb0, a.vs.st, cur, vc);
     kok = key_ok(cur);
     iql = qr.finish(a.eps);
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      qb[ks] = qr.q.f[ks];
-      hb[ks] = qr.dh.f[ks];
-    }
-  }
-  {  // dh and 1/|q| of this unit's rows for dkdv_kernel (zero past Tq)
+    // dh and 1/|q| of this unit's rows for dkdv_kernel (zero past Tq)
     T* dst = (T*)a.dh + ((int64_t)bh * a.Tq_pad + i) * DP;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) *reinterpret_cast<frag*>(dst + KS * ks + PER * half) = hb[ks];
+    for (int ks = 0; ks < NKS; ++ks) {
+      qh[ks][lane] = qr.q.f[ks];
+      qh[NKS + ks][lane] = qr.dh.f[ks];
+      *reinterpret_cast<frag*>(dst + KS * ks + PER * half) = qr.dh.f[ks];
+    }
     if (half == 0) a.iqs[(int64_t)bh * a.Tq_pad + i] = valid ? iql : 0.0f;
   }
   const float thq = hp.thr / iql;  // s > thr  <=>  (q . k)/|k| > thr |q|
@@ -284,15 +285,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
 
   for (;;) {
     const int k0 = cur * kUnit;
-    // the next unit's rows load while this one is computed (past the last
-    // unit, the current one again, a cache hit: every iteration then waits
-    // for the same count)
     const int nxt = walk.next();
-    const int nl = nxt >= 0 ? nxt : cur;
-    frag kn[NKS], vn[NKS];
-    load_rows(kb0, a.ks.st, nl, kn);
-    load_rows(vb0, a.vs.st, nl, vn);
-    const bool kokn = key_ok(nl);
     zero_tail(kc);
     zero_tail(vc);
     // register r -> key k0 + rowof(r, half), lane -> query i
@@ -300,15 +293,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     float s2k = 0.0f, s2v = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.0f; dp[r] = 0.0f; }
+    {
+      frag g[NKS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      s = M::mma_ng(kc[ks], qb[ks], s);
-      s2k = frag_dot(kc[ks], kc[ks], s2k);
-    }
+      for (int ks = 0; ks < NKS; ++ks) g[ks] = qh[ks][lane];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      dp = M::mma_ng(vc[ks], hb[ks], dp);
-      s2v = frag_dot(vc[ks], vc[ks], s2v);
+      for (int ks = 0; ks < NKS; ++ks) {
+        s = M::mma_ng(kc[ks], g[ks], s);
+        s2k = frag_dot(kc[ks], kc[ks], s2k);
+      }
+      guard_frags(g);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) g[ks] = qh[NKS + ks][lane];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        dp = M::mma_ng(vc[ks], g[ks], dp);
+        s2v = frag_dot(vc[ks], vc[ks], s2v);
+      }
+      guard_frags(g);
     }
     guard_frags(vc);
     s2k = half_sum(s2k);
@@ -383,16 +385,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     guard_frags(db);
     if (nxt < 0) break;
     cur = nxt;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      kc[ks] = kn[ks];
-      vc[ks] = vn[ks];
-    }
-    kok = kokn;
+    load_rows(kb0, a.ks.st, cur, kc);
+    load_rows(vb0, a.vs.st, cur, vc);
+    kok = key_ok(cur);
   }
-  guard_frags(qb);
-  guard_frags(hb);
-  write_norm_bwd<T, DP>(adq, qb, valid, a.D, a.eps, half, dqrow);
+  {
+    frag x[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) x[ks] = qh[ks][lane];
+    write_norm_bwd<T, DP>(adq, x, valid, a.D, a.eps, half, dqrow);
+  }
   dr_acc = wave_sum(dr_acc);
   dw_acc = wave_sum(dw_acc);
   if (lane == 0) {
