@@ -601,6 +601,28 @@ __device__ inline void xcd_interleave(int& bx, int& by) {
   }
 }
 
+// xcd_interleave with the heads taken widest window first.  Heads are (b, h)
+// b-major and the window depends on h only, so logical head row by = r*B + b
+// becomes (b, h of window rank r).  A unit's cost grows with its head's
+// window, and blocks run in dispatch order, so the longest units no longer
+// start last (the kernel would end with a few of them running alone).  Ties
+// keep index order; more than 64 heads per batch keep plain order.  Called by
+// every lane of a one-wave block.
+__device__ inline void xcd_interleave_ranked(const float* w, int H, int& bx, int& by) {
+  xcd_interleave(bx, by);
+  const int BH = (int)gridDim.y;
+  if (H > 64 || BH % H != 0) return;
+  const int B = BH / H, r = by / B, b = by % B;
+  const int lane = threadIdx.x & 63;
+  const float wl = lane < H ? w[lane] : 0.0f;  // lane o holds head o's window
+  int rank = 0;
+  for (int o = 0; o < H; ++o) {
+    const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), o));
+    rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
+  }
+  by = b * H + (int)__builtin_ctzll(__ballot(lane < H && rank == r));
+}
+
 // XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs
 // in linear order (x fastest); when the grid divides evenly, remap so each
 // XCD receives a contiguous run of logical blocks (the query tiles of the same

@@ -426,7 +426,7 @@ void fwd_live_kernel(FwdKArgs a) {
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
-  xcd_interleave(qu, bh);
+  xcd_interleave_ranked(a.w, a.H, qu, bh);
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);
