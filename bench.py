@@ -47,6 +47,20 @@ def parse():
     return p.parse_args()
 
 
+def cfg2_inputs(seed=0):
+    """BASELINE.json configs[1] inputs, drawn on the CPU so every consumer (this
+    bench, the full-shape parity test) sees identical values: q, k, v, dO ~
+    N(0,1) of shape (B,T,H,D) = (4,8192,8,64) rounded to bf16, r_h ~ U[1.9,2.1],
+    w_h ~ U[256,8192] (lists of H floats), all from torch.Generator(seed)."""
+    import torch
+    B, T, H, D = 4, 8192, 8, 64
+    g = torch.Generator().manual_seed(seed)
+    r = (1.9 + 0.2 * torch.rand(H, generator=g)).tolist()
+    w = (256.0 + (8192.0 - 256.0) * torch.rand(H, generator=g)).tolist()
+    q, k, v, dy = (torch.randn(B, T, H, D, generator=g).bfloat16() for _ in range(4))
+    return q, k, v, dy, r, w
+
+
 def window_tiles(T, w_list, tile=64):
     """|W|: causal 64x64 tiles holding a pair with 0 <= i-j < w, per (b,h) summed over heads."""
     n = 0
@@ -188,12 +202,9 @@ def main():
     torch.manual_seed(args.seed)
     dev = torch.device("cuda:0")
 
-    B, T, H, D = 4, 8192, 8, 64
-    g = torch.Generator().manual_seed(args.seed)
-    r = (1.9 + 0.2 * torch.rand(H, generator=g)).tolist()
-    w = (256.0 + (8192.0 - 256.0) * torch.rand(H, generator=g)).tolist()
-    gd = torch.Generator(device="cuda").manual_seed(args.seed)
-    q, k, v, dy = (torch.randn(B, T, H, D, device=dev, generator=gd).bfloat16() for _ in range(4))
+    q, k, v, dy, r, w = cfg2_inputs(args.seed)
+    B, T, H, D = q.shape
+    q, k, v, dy = (t.to(dev) for t in (q, k, v, dy))
     rg = torch.tensor(r, device=dev)
     wg = torch.tensor(w, device=dev)
 

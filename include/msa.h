@@ -24,6 +24,10 @@
  *   y, dy, dq, dk, dv : contiguous (B, T, H, D), i.e. the (B,T,d_model) layout
  *             out_proj consumes (attention.py:198-200).
  *   r, w    : fp32 (H,), r = exp(s_r)+1, w = exp(s_v)+1 (attention.py:164-165).
+ *             Precondition r >= 1 (which r = exp(s_r)+1 always meets): padded
+ *             and masked keys enter with s = 0, which gives alpha = 0 only
+ *             when r >= 1.  A window that is NaN or not positive is treated as
+ *             empty (zero output for that head; the reference gives NaN).
  *   key_padding_mask : nullable uint8 (B, Tk), nonzero = ignore key.
  *   dtype   : MSA_F32 or MSA_BF16 for q,k,v,y,dy,dq,dk,dv.
  *   dropout_p, dropout_seed : attention dropout on alpha*m (attention.py:68,
@@ -84,10 +88,10 @@ size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
  * ceil(2*nkt/32) words; key unit ku is bit ku%32 of word ku/32 of the row. */
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);
 
-/* Bytes of backward workspace: one (dr, dw) partial per (b, h, 32-key unit),
- * summed in a fixed order, plus dh = TanhNorm'(h)^T dy and 1/|q| per query
- * row (padded to 64 rows per tile), which the dQ pass hands to the dK/dV
- * pass. */
+/* Bytes of backward workspace: one (dr, dw) partial per (b, h, 32-query
+ * unit), summed in a fixed order, plus dh = TanhNorm'(h)^T dy and 1/|q| per
+ * query row (padded to 64 rows per tile), which the dQ pass hands to the
+ * dK/dV pass. */
 size_t msa_bwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
 /*

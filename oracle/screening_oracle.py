@@ -347,3 +347,127 @@ def tile_counts(q, k, r, w, causal=True, eps=EPS, tile=64, key_padding_mask=None
         win[:, :, q0:q0 + -(-(i1 - i0) // tile)] |= tiles(inside)
         act[:, :, q0:q0 + -(-(i1 - i0) // tile)] |= tiles(live)
     return int(win.sum()), int(act.sum()), act
+
+
+# ---------------------------------------------------------------------------
+# Live-pair form, for full-size checks (e.g. B=4, T=8192 or T=100,000).
+#
+# alpha_ij = relu(1 - r(1 - s_ij))^2 is zero unless s_ij > 1 - 1/r
+# (attention.py:75-90), and at the benchmark shapes almost every pair is
+# below that threshold.  live_pairs() lists the pairs that pass, and
+# sparse_forward_backward() evaluates forward() and backward() over exactly
+# those pairs in float64, so its outputs are those of the dense functions
+# (sums in a different order) at a cost linear in the number of live pairs.
+# ---------------------------------------------------------------------------
+
+# Candidate margin of the float32 screening pass.  Each unit vector is
+# rounded to float32 (relative error 2^-24 per component) and the 64-term
+# dot product accumulates in float32, so |s32 - s| <= (D + 2) * 2^-24 *
+# sum_d |q^_d k^_d| <= 130 * 6e-8 < 1e-5 for D <= 128 (sum_d |q^_d k^_d| <= 1
+# for unit vectors).  A margin of 1e-4 therefore keeps every pair whose exact
+# s passes; the exact float64 test then decides.
+SCREEN_MARGIN = 1e-4
+
+
+def live_pairs(q, k, r, w, causal=True, eps=EPS, key_padding_mask=None, block=1024):
+    """Every in-window, unmasked pair (b, h, i, j) with 1 - r_h(1 - s_ij) > 0.
+
+    Returns a dict of equal-length arrays: b, h, i, j (int64) and s (float64,
+    s_ij = q^_i . k^_j).  Window and padding follow attention.py:111-118,
+    :174-183 and :185-188.  Candidates come from a float32 pass over the
+    window only (SCREEN_MARGIN bounds its error); the kept pairs are decided
+    in float64."""
+    qn, kn = normalize(_heads(q), eps), normalize(_heads(k), eps)
+    B, H, Tq, D = qn.shape
+    Tk = kn.shape[2]
+    qn32, kn32 = qn.astype(np.float32), kn.astype(np.float32)
+    r = np.asarray(r, dtype=np.float64).reshape(H)
+    w = np.asarray(w, dtype=np.float64).reshape(H)
+    kpm = None if key_padding_mask is None else np.asarray(key_padding_mask, dtype=bool)
+    out = {n: [] for n in ("b", "h", "i", "j", "s")}
+    for hh in range(H):
+        thr = 1.0 - 1.0 / r[hh]
+        wc = math.ceil(w[hh]) if math.isfinite(w[hh]) and w[hh] < 2 ** 40 else 2 ** 40
+        for b in range(B):
+            for i0, i1 in _blocks(Tq, block):
+                lo = max(0, i0 - wc + 1)
+                hi = min(Tk, i1 if causal else i1 + wc - 1)
+                if hi <= lo:
+                    continue
+                s32 = qn32[b, hh, i0:i1] @ kn32[b, hh, lo:hi].T
+                ii, jj = np.nonzero(s32 > np.float32(thr - SCREEN_MARGIN))
+                ii = ii.astype(np.int64) + i0
+                jj = jj.astype(np.int64) + lo
+                rel = ii - jj                       # i - j
+                inside = ((rel >= 0) & (rel < w[hh])) if causal else (np.abs(rel) < w[hh])
+                if kpm is not None:
+                    inside &= ~kpm[b, jj]
+                ii, jj = ii[inside], jj[inside]
+                s = np.einsum("pd,pd->p", qn[b, hh, ii], kn[b, hh, jj])
+                keep = 1.0 - r[hh] * (1.0 - s) > 0.0
+                n = int(keep.sum())
+                out["b"].append(np.full(n, b, dtype=np.int64))
+                out["h"].append(np.full(n, hh, dtype=np.int64))
+                out["i"].append(ii[keep])
+                out["j"].append(jj[keep])
+                out["s"].append(s[keep])
+    return {n: (np.concatenate(v) if v else np.zeros(0, dtype=np.float64 if n == "s" else np.int64))
+            for n, v in out.items()}
+
+
+def sparse_forward_backward(q, k, v, r, w, dy=None, causal=True, eps=EPS, key_padding_mask=None,
+                            dropout=None, pairs=None):
+    """forward() and, when dy is given, backward() evaluated over the live pairs only.
+
+    Returns (y, grads, pairs): y (B,Tq,H,D); grads = (dq, dk, dv, dr, dw) as
+    backward() returns them, or None without dy; pairs = live_pairs(...).
+    Same math and conventions as forward()/backward(), float64 throughout."""
+    import scipy.sparse as sp
+    if pairs is None:
+        pairs = live_pairs(q, k, r, w, causal, eps, key_padding_mask)
+    qh, kh, vh = _heads(q), _heads(k), _heads(v)
+    qn, kn, vn = normalize(qh, eps), normalize(kh, eps), normalize(vh, eps)
+    B, H, Tq, D = qn.shape
+    Tk = kn.shape[2]
+    r = np.asarray(r, dtype=np.float64).reshape(H)
+    w = np.asarray(w, dtype=np.float64).reshape(H)
+    pb, ph, pi, pj, s = pairs["b"], pairs["h"], pairs["i"], pairs["j"], pairs["s"]
+    a = 1.0 - r[ph] * (1.0 - s)                      # > 0 on every listed pair
+    rel = (pj - pi).astype(np.float64)               # j - i
+    m = 0.5 * (np.cos(math.pi * rel / w[ph]) + 1.0)
+    mdw = 0.5 * np.sin(math.pi * rel / w[ph]) * math.pi * rel / (w[ph] * w[ph])
+    if dropout is not None and float(dropout[0]) > 0.0:
+        p_, seed = dropout
+        keep = dropout_keep_bits(seed, pb * H + ph, pi, pj) >= np.uint64(dropout_threshold(p_))
+        c = np.where(keep, dropout_scale(p_), 0.0)
+        m = m * c
+        mdw = mdw * c
+    p = a * a * m
+    row = (pb * H + ph) * Tq + pi                    # into (B*H*Tq) rows
+    col = (pb * H + ph) * Tk + pj                    # into (B*H*Tk) rows
+    shape = (B * H * Tq, B * H * Tk)
+    P = sp.csr_matrix((p, (row, col)), shape=shape)
+    qf, kf, vf = qn.reshape(-1, D), kn.reshape(-1, D), vn.reshape(-1, D)
+    h = np.asarray(P @ vf).reshape(B, H, Tq, D)
+    n = np.sqrt(np.sum(h * h, axis=-1, keepdims=True))
+    nc = np.maximum(n, eps)
+    F = np.tanh(nc) / nc
+    y = np.transpose(F * h, (0, 2, 1, 3))
+    if dy is None:
+        return y, None, pairs
+    g = _heads(dy)
+    G = _tanhnorm_g(nc)
+    hd = np.sum(h * g, axis=-1, keepdims=True)
+    dh = np.where(n > eps, F * g + G * hd * h, (math.tanh(eps) / eps) * g).reshape(-1, D)
+    dP = np.einsum("pd,pd->p", dh[row], vf[col])
+    ds = 2.0 * a * r[ph] * m * dP
+    DS = sp.csr_matrix((ds, (row, col)), shape=shape)
+    dqn = np.asarray(DS @ kf).reshape(B, H, Tq, D)
+    dkn = np.asarray(DS.T @ qf).reshape(B, H, Tk, D)
+    dvn = np.asarray(P.T @ dh).reshape(B, H, Tk, D)
+    dr = np.bincount(ph, weights=-2.0 * a * (1.0 - s) * m * dP, minlength=H)
+    dw = np.bincount(ph, weights=a * a * mdw * dP, minlength=H)
+    t = lambda x: np.transpose(x, (0, 2, 1, 3))
+    grads = (t(_normalize_bwd(qh, dqn, eps)), t(_normalize_bwd(kh, dkn, eps)),
+             t(_normalize_bwd(vh, dvn, eps)), dr, dw)
+    return y, grads, pairs

@@ -367,6 +367,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
     frag db[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) db[c] = M::pack(dp, c * PER);
+    frag id[NC];  // identity slices, held (and guarded) as named operands
+#pragma unroll
+    for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk) {
       frag kt[NC];
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
 #pragma unroll
       for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) tr = M::mma_ng(kc[dblk * NC + c], ident_frag<T>(c, lane), tr);
+      for (int c = 0; c < NC; ++c) tr = M::mma_ng(kc[dblk * NC + c], id[c], tr);
 #pragma unroll
       for (int c = 0; c < NC; ++c) kt[c] = M::pack(tr, c * PER);
 #pragma unroll
@@ -383,6 +386,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
     }
     guard_frags(kc);
     guard_frags(db);
+    guard_frags(id);
     if (nxt < 0) break;
     cur = nxt;
     load_rows(kb0, a.ks.st, cur, kc);
@@ -612,11 +616,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
     // with dH^T, Q^T from identity products on the row registers, one
     // 32-column block of d at a time
-    frag pb[NC], db[NC];
+    frag pb[NC], db[NC], id[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       pb[c] = M::pack(s, c * PER);
       db[c] = M::pack(dp, c * PER);
+      id[c] = ident_frag<T>(c, lane);  // held (and guarded) as named operands
     }
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk) {
@@ -628,7 +633,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
         for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
-          tr = M::mma_ng(op == 0 ? hf[dblk * NC + c] : qf[dblk * NC + c], ident_frag<T>(c, lane), tr);
+          tr = M::mma_ng(op == 0 ? hf[dblk * NC + c] : qf[dblk * NC + c], id[c], tr);
 #pragma unroll
         for (int c = 0; c < NC; ++c) t[c] = M::pack(tr, c * PER);
 #pragma unroll
@@ -643,6 +648,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     guard_frags(hf);
     guard_frags(pb);
     guard_frags(db);
+    guard_frags(id);
     if (nxt < 0) break;
     cur = nxt;
 #pragma unroll

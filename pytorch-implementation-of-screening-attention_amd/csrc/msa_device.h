@@ -208,17 +208,19 @@ struct HeadParams {
 // In-window distances dd = i - j (attention.py:111-118 causal, :176-181
 // non-causal): causal 0 <= dd < wc, i.e. shift 0 and limit wc; non-causal
 // -wc < dd < wc, i.e. shift wc-1 and limit 2wc-1.  Positions stay below 2^22
-// and wc <= 2^30, so dd + wsh never overflows.
+// and wc <= 2^30, so dd + wsh never overflows.  A window that is not a number
+// (or not positive) is empty: wc = 0, limit 0, so no pair of the head is live
+// and its outputs are zero (the reference's dense path gives NaN there).
 __device__ inline HeadParams head_params(const float* r, const float* w, int h, bool causal) {
   HeadParams p;
   p.r = r[h];
   p.w = w[h];
   p.iw = 1.0f / p.w;
-  float c = ceilf(p.w);
-  p.wc = c > 1073741824.0f ? 1073741824 : (int)c;
+  const float c = ceilf(p.w);
+  p.wc = !(c > 0.0f) ? 0 : (c > 1073741824.0f ? 1073741824 : (int)c);
   p.thr = 1.0f - 1.0f / p.r - 1e-6f;
   p.wsh = causal ? 0 : p.wc - 1;
-  p.wlim = causal ? (unsigned)p.wc : (unsigned)(2 * p.wc - 1);
+  p.wlim = p.wc == 0 ? 0u : (causal ? (unsigned)p.wc : (unsigned)(2 * p.wc - 1));
   return p;
 }
 
@@ -608,19 +610,29 @@ __device__ inline void xcd_interleave(int& bx, int& by) {
 // start last (the kernel would end with a few of them running alone).  Ties
 // keep index order; more than 64 heads per batch keep plain order.  Called by
 // every lane of a one-wave block.
-__device__ inline void xcd_interleave_ranked(const float* w, int H, int& bx, int& by) {
-  xcd_interleave(bx, by);
-  const int BH = (int)gridDim.y;
-  if (H > 64 || BH % H != 0) return;
-  const int B = BH / H, r = by / B, b = by % B;
+//
+// Ranks come from a total order, (window key, head index) with a NaN window
+// keyed as +inf, so the ranks 0..H-1 are a permutation of the heads whatever
+// the windows hold (NaN, infinities, duplicates): every (b, h) gets exactly
+// one block row.  head_rank_select() returns the head of rank r.
+__device__ inline float window_rank_key(float w) { return w != w ? INFINITY : w; }
+__device__ inline int head_rank_select(const float* w, int H, int r) {
   const int lane = threadIdx.x & 63;
-  const float wl = lane < H ? w[lane] : 0.0f;  // lane o holds head o's window
+  const float wl = window_rank_key(lane < H ? w[lane] : 0.0f);  // lane o holds head o's key
   int rank = 0;
   for (int o = 0; o < H; ++o) {
     const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), o));
     rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
   }
-  by = b * H + (int)__builtin_ctzll(__ballot(lane < H && rank == r));
+  const unsigned long long sel = __ballot(lane < H && rank == r);
+  return sel != 0ull ? (int)__builtin_ctzll(sel) : r;  // sel is never empty: ranks are a permutation
+}
+__device__ inline void xcd_interleave_ranked(const float* w, int H, int& bx, int& by) {
+  xcd_interleave(bx, by);
+  const int BH = (int)gridDim.y;
+  if (H > 64 || BH % H != 0) return;
+  const int B = BH / H, r = by / B, b = by % B;
+  by = b * H + head_rank_select(w, H, r);
 }
 
 // XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs

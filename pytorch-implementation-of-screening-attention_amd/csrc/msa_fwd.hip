@@ -140,14 +140,17 @@ __device__ inline void screen_order(const FwdKArgs& a, int& bx, int& bh) {
   const int x = p & 7, s = p >> 3;
   const int jh = s / nx;                                 // this XCD's jh-th head
   const int k = 8 * jh + ((jh & 1) ? 7 - x : x);         // its rank, widest first
+  // ranks on the total order (window key, index) of window_rank_key: a
+  // permutation of the B*H heads even with NaN or repeated windows
   const int lane = threadIdx.x & 63;
-  const float wl = lane < BH ? a.w[lane % a.H] : 0.0f;  // lane o holds head o's window
+  const float wl = window_rank_key(lane < BH ? a.w[lane % a.H] : 0.0f);  // lane o holds head o's key
   int rank = 0;
   for (int o = 0; o < BH; ++o) {
     const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), o));
     rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
   }
-  bh = __builtin_ctzll(__ballot(lane < BH && rank == k));
+  const unsigned long long sel = __ballot(lane < BH && rank == k);
+  bh = sel != 0ull ? (int)__builtin_ctzll(sel) : k;  // never empty: ranks are a permutation
   bx = nx - 1 - (s - jh * nx);
 }
 

@@ -27,7 +27,7 @@ struct Strides3 { int64_t sb, st, sh; };
 // padded and masked keys) that the forward stages through LDS.
 size_t fwd_ws_bytes(const Geometry& g);
 
-// Backward workspace: per-key-unit partial sums of dr, dw ([2][b*h][2*nkt]
+// Backward workspace: per-query-unit partial sums of dr, dw ([2][b*h][2*nqt]
 // fp32), then dh ([b*h][Tq_pad][DP] in the input type) and 1/|q|
 // ([b*h][Tq_pad] fp32) that dq_kernel hands to dkdv_kernel.
 size_t bwd_ws_bytes(const Geometry& g);

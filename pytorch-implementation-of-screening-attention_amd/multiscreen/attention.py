@@ -132,7 +132,9 @@ class ScreeningAttention(nn.Module):
         kc, vc = cache.k[:, :pos + 1], cache.v[:, :pos + 1]
         w, r = self.window(), self.sharpness()
         if x.is_cuda:
-            y = ops.decode_step(q[:, 0], cache.k, cache.v, pos + 1, r, w, self.eps, cache.workspace)
+            # the cache's dtype is the kernel's (fp16 models keep an fp32 cache)
+            y = ops.decode_step(q[:, 0].to(cache.k.dtype), cache.k, cache.v, pos + 1, r, w, self.eps,
+                                cache.workspace).to(x.dtype)
         else:
             y = screening_core_dense(q, kc, vc, r, w, True, self.eps, q_offset=pos)[:, 0]
         return self.out_proj(y.reshape(B, 1, self.d_model))
@@ -143,9 +145,12 @@ class KVCache:
 
     Stored head-major, (B, H, capacity, D), so that one head's window is one
     contiguous stream for the decode kernel; `k` and `v` are the (B, capacity,
-    H, D) views of that storage, the layout of the projections."""
+    H, D) views of that storage, the layout of the projections.  The kernels
+    compute in float32 or bfloat16, so a float16 model's cache is float32."""
 
     def __init__(self, batch, capacity, num_heads, head_dim, dtype, device):
+        if dtype == torch.float16:
+            dtype = torch.float32
         self._k = torch.zeros((batch, num_heads, capacity, head_dim), dtype=dtype, device=device)
         self._v = torch.zeros_like(self._k)
         self.k = self._k.permute(0, 2, 1, 3)

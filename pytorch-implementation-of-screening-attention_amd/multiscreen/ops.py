@@ -107,6 +107,8 @@ def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, dy, key_padding_mask=Non
     """One msa_bwd call.  Returns (dq, dk, dv, dr, dw); dq/dk/dv in (B,T,H,D).
     dropout_p / seed must be the forward's."""
     L = _native.lib()
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"q/k/v must share dtype float32 or bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
     dt = _DTYPES[q.dtype]
     es = q.element_size()
     q, k, v = _as_bthd(q, "q", es), _as_bthd(k, "k", es), _as_bthd(v, "v", es)
@@ -179,6 +181,9 @@ def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None):
     L = _native.lib()
     if not q.is_cuda:
         raise RuntimeError("decode_step runs on the GPU only (got a CPU tensor)")
+    if q.dtype not in _DTYPES or kcache.dtype != q.dtype or vcache.dtype != q.dtype:
+        raise TypeError(f"decode_step needs q and the caches in one of float32 / bfloat16, got "
+                        f"{q.dtype}, {kcache.dtype}, {vcache.dtype}")
     dt = _DTYPES[q.dtype]
     B, H, D = q.shape
     if q.stride(2) != 1:

@@ -128,6 +128,14 @@ class TestMultiscreenLM:
         assert torch.equal(got, ids)
 
 
+def test_float16_model_keeps_a_float32_cache():
+    # the kernels compute in float32 or bfloat16: a float16 model's KV cache is
+    # float32 (decode casts its query to the cache dtype and back)
+    from multiscreen.attention import KVCache
+    c = KVCache(2, 8, 4, 16, torch.float16, "cpu")
+    assert c.k.dtype == torch.float32 and c.v.shape == (2, 8, 4, 16)
+
+
 def test_lm_matches_reference_golden():
     z = load_golden("lm_tiny")
     torch.manual_seed(0)

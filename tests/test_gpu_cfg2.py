@@ -1,0 +1,75 @@
+"""The timed workload at its own shape: BASELINE.json configs[1] (B=4, T=8192,
+H=8, D=64, bf16, causal, r ~ U[1.9,2.1], w ~ U[256,8192]) forward AND
+backward through the C ABI, every output tensor compared in full with the
+float64 oracle evaluated over the live pairs (oracle.sparse_forward_backward,
+pinned against the dense oracle in tests/test_oracle.py).
+
+Inputs are bench.py's own (bench.cfg2_inputs, the bench's seed).  The
+"sharpened" variant lowers r on two heads (r = 1.6, 1.75) so that about 10^5
+pairs are live and every gradient is far from vacuous; the literal variant
+has about 8,000.  Tolerance: max|got - ref| / max|ref| <= 2e-2 per tensor
+(bf16).  At T = 8192 with windows up to 8192 (256 32-key units) these runs
+take the paths shorter tests do not: 8-word bitmap rows, bitmap columns at
+key units >= 64 and the dr/dw sums over B*256 query-unit shares.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+import screening_oracle as O
+from helpers import np64, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _unit_bits(bits, B, H, T):
+    n = T // 32
+    words = (n + 31) // 32
+    b = bits.cpu().numpy().view(np.uint32)[:B * H * n * words].reshape(B, H, n, words)
+    got = np.zeros((B, H, n, n), dtype=bool)
+    for ku in range(n):
+        got[..., ku] = (b[..., ku // 32] >> (ku % 32)) & 1
+    return got
+
+
+@pytest.mark.parametrize("variant", ["literal", "sharpened"])
+def test_cfg2_full_shape_forward_backward(variant):
+    from multiscreen import ops
+    q, k, v, dy, r, w = bench.cfg2_inputs(0)
+    if variant == "sharpened":
+        r[0], r[1] = 1.6, 1.75
+    B, T, H, D = q.shape
+    _say(f"cfg2 {variant}: B={B} T={T} H={H} D={D} r={np.round(r, 4).tolist()} w={np.round(w, 1).tolist()}")
+    dev = "cuda"
+    rg, wg = torch.tensor(r, device=dev), torch.tensor(w, device=dev)
+    qd, kd, vd, dyd = (t.to(dev) for t in (q, k, v, dy))
+    y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, True, 1e-8, None)
+    dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, True, 1e-8, y, hnorm, bits, dyd)
+    torch.cuda.synchronize()
+    _say("cfg2: GPU forward + backward done")
+    got = {n: np64(t) for n, t in zip(("y", "dq", "dk", "dv", "dr", "dw"), (y, dq, dk, dv, dr, dw))}
+    units = _unit_bits(bits, B, H, T)
+    del qd, kd, vd, dyd, y, hnorm, bits, dq, dk, dv
+    rr, ww = np.array(r, dtype=np.float64), np.array(w, dtype=np.float64)
+    yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), True)
+    _say(f"cfg2: oracle done, {len(P['i'])} live pairs")
+    assert len(P["i"]) > (50000 if variant == "sharpened" else 2000)
+    for name, want in zip(("y", "dq", "dk", "dv", "dr", "dw"), (yref,) + tuple(gref)):
+        assert np.max(np.abs(want)) > 0, f"{name} vacuous"
+        e = rel_err(got[name], want)
+        _say(f"cfg2 {variant}: {name} rel err {e:.3e}")
+        assert e <= TOL, f"{name}: rel err {e:.3e} > {TOL}"
+    # every pair whose alpha is not within rounding of the threshold lies in a
+    # unit the forward marked live; unmarked units hold only such pairs
+    a = 1.0 - rr[P["h"]] * (1.0 - P["s"])
+    clear = a > 1e-2
+    marked = units[P["b"], P["h"], P["i"] // 32, P["j"] // 32]
+    assert np.all(marked[clear])

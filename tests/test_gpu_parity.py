@@ -72,6 +72,12 @@ FWD_CASES = [
     # head_dim 32: the instantiation where an unguarded MFMA source-register
     # hazard once corrupted dq/dk (see the guard in msa_device.h)
     (1, 128, 128, 2, 32, True, [1.1, 1.25], [20.0, 400.0], False),
+    # causal with Tq != Tk: both index ranges start at 0 (attention.py:108-118,
+    # :171-173), so queries past Tk see the last keys and keys past Tq are seen
+    # by no query
+    (1, 100, 160, 2, 64, True, [1.1, 1.3], [30.0, 500.0], False),          # Tq < Tk
+    (2, 190, 90, 2, 64, True, [1.15, 1.25], [60.0, 1e4], True),            # Tq > Tk, key padding
+    (1, 64, 300, 3, 32, True, [1.1, 1.2, 1.4], [2.0, 100.0, 1e6], False),   # one query tile, five key tiles
 ]
 
 
@@ -355,3 +361,63 @@ def test_cfg2_full_size_sampled_rows_bf16():
     yref = O.rows_forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), rows, True)
     assert np.max(np.abs(yref)) > 1e-3
     assert rel_err(np64(y[:, rows]), yref) <= 2e-2
+
+
+def test_float16_model_generate():
+    # a float16 model (model.half()) decodes through float32 caches; its greedy
+    # tokens are those of re-running forward() on the prefix
+    from multiscreen import MultiscreenLM
+    torch.manual_seed(0)
+    lm = MultiscreenLM(vocab_size=50, d_model=64, num_heads=4, num_layers=2, max_seq_len=64)
+    for blk in lm.blocks:
+        with torch.no_grad():
+            blk.attn.s_r.fill_(math.log(0.15))
+            blk.attn.s_v.copy_(torch.log(torch.tensor([2.0, 7.0, 20.0, 60.0])))
+    lm = lm.half().to(DEV)
+    prompt = torch.randint(0, 50, (2, 5), device=DEV)
+    got = lm.generate(prompt, max_new_tokens=6, top_k=1)
+    assert got.shape == (2, 11)
+    ids = prompt
+    with torch.no_grad():
+        for _ in range(6):
+            nxt = lm(ids)["logits"][:, -1].argmax(-1, keepdim=True)
+            ids = torch.cat([ids, nxt], 1)
+    assert torch.equal(got, ids)
+
+
+def _rank_permutation(w):
+    """Host restatement of the kernels' head ranking (window_rank_key and the
+    (key, index) order of msa_device.h): rank of head o among the heads."""
+    key = [math.inf if x != x else x for x in w]
+    return [sum(1 for p in range(len(w)) if key[p] > key[o] or (key[p] == key[o] and p < o))
+            for o in range(len(w))]
+
+
+def test_nan_window_is_contained():
+    # a NaN window (s_v diverged) must not fault or disturb other heads: the
+    # head ranking stays a permutation, the NaN head's window is empty (its
+    # output is zero where the reference's is NaN), and every other head's
+    # output and gradients are bitwise those of a run with a finite window
+    assert sorted(_rank_permutation([float("nan"), 3.0, float("nan"), 3.0, math.inf, -math.inf, 0.0, -0.0])) == \
+        list(range(8))
+    B, T, H, D = 2, 256, 8, 64
+    q, k, v = correlated_qkv(B, T, T, H, D, seed=8, dtype=torch.bfloat16, rho=0.35)
+    dy = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(2)).bfloat16().to(DEV)
+    r = [1.1, 1.2, 1.15, 1.3, 1.1, 1.25, 1.2, 1.1]
+    w_ok = [40.0, 2.0, 100.0, 100.0, 1e5, 7.5, 300.0, 60.0]
+    w_nan = list(w_ok)
+    w_nan[2] = float("nan")
+    ops = _ops()
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = []
+    for w in (w_ok, w_nan):
+        rg, wg = _rw(H, r, w)
+        y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, True, 1e-8, None)
+        outs.append((y,) + ops.bwd_raw(qd, kd, vd, rg, wg, True, 1e-8, y, hnorm, bits, dy))
+    torch.cuda.synchronize()
+    keep = [h for h in range(H) if h != 2]
+    for a, b in zip(outs[0][:4], outs[1][:4]):          # y, dq, dk, dv
+        assert torch.equal(a[:, :, keep], b[:, :, keep])
+    assert torch.count_nonzero(outs[1][0][:, :, 2]) == 0
+    for a, b in zip(outs[0][4:], outs[1][4:]):          # dr, dw
+        assert torch.equal(a[keep], b[keep])

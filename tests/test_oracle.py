@@ -244,3 +244,99 @@ def test_oracle_matches_reference_golden(name):
     # s_r, s_v enter through r = exp(s_r)+1, w = exp(s_v)+1
     np.testing.assert_allclose(dr * (r - 1.0), z["ds_r"], rtol=2e-4, atol=1e-7 * max(1, abs(z["ds_r"]).max()))
     np.testing.assert_allclose(dw * (w - 1.0), z["ds_v"], rtol=2e-4, atol=1e-7 * max(1, abs(z["ds_v"]).max()))
+
+
+# ---------------------------------------------------------------------------
+# live-pair form (full-size checks): pinned against the dense functions above
+# ---------------------------------------------------------------------------
+def _dense_live_set(q, k, r, w, causal, kpm=None):
+    qn = q / np.linalg.norm(q, axis=-1, keepdims=True)
+    kn = k / np.linalg.norm(k, axis=-1, keepdims=True)
+    B, Tq, H, _ = q.shape
+    Tk = k.shape[1]
+    out = set()
+    for b in range(B):
+        for h in range(H):
+            s = qn[b, :, h] @ kn[b, :, h].T
+            for i in range(Tq):
+                for j in range(Tk):
+                    d = i - j
+                    inside = (0 <= d < w[h]) if causal else (abs(d) < w[h])
+                    if inside and not (kpm is not None and kpm[b, j]) and 1 - r[h] * (1 - s[i, j]) > 0:
+                        out.add((b, h, i, j))
+    return out
+
+
+@pytest.mark.parametrize("causal,Tq,Tk,kpm", [(True, 70, 70, False), (True, 90, 50, True),
+                                               (True, 40, 95, False), (False, 60, 110, True)])
+def test_live_pairs_equal_dense_set(causal, Tq, Tk, kpm):
+    B, H, D = 2, 3, 16
+    q, k = rnd((B, Tq, H, D), 40), rnd((B, Tk, H, D), 41)
+    q[..., 0] += 1.0
+    k[..., 0] += 1.0
+    r, w = np.array([1.1, 1.5, 2.0]), np.array([3.5, 20.0, 1e6])
+    mask = None
+    if kpm:
+        mask = np.zeros((B, Tk), dtype=bool)
+        mask[0, ::7] = True
+        mask[1, -4:] = True
+    P = O.live_pairs(q, k, r, w, causal, key_padding_mask=mask, block=32)
+    got = set(zip(P["b"].tolist(), P["h"].tolist(), P["i"].tolist(), P["j"].tolist()))
+    want = _dense_live_set(q, k, r, w, causal, mask)
+    assert len(want) > 100 and got == want
+    assert len(got) == len(P["i"])          # no pair listed twice
+
+
+def test_live_pairs_keep_pairs_just_above_threshold():
+    # s a few float32 ulps above 1 - 1/r: the float32 candidate pass must not
+    # drop it (SCREEN_MARGIN); s just below must not be listed
+    r = 1.7
+    thr = 1.0 - 1.0 / r
+    D = 64
+    q = np.zeros((1, 3, 1, D))
+    q[..., 0] = 1.0
+    k = np.zeros((1, 3, 1, D))
+    for j, c in enumerate((thr + 3e-8, thr - 3e-8, thr + 1e-3)):
+        k[0, j, 0, 0] = c
+        k[0, j, 0, 1] = math.sqrt(1.0 - c * c)
+    P = O.live_pairs(q, k, np.array([r]), np.array([1e9]), True)
+    assert sorted(zip(P["i"].tolist(), P["j"].tolist())) == [(0, 0), (1, 0), (2, 0), (2, 2)]
+
+
+def test_live_pairs_screen_margin_bound():
+    # the float32 candidate pass is within a tenth of SCREEN_MARGIN of float64
+    for D, seed in ((64, 42), (128, 43), (16, 44)):
+        x = rnd((400, D), seed)
+        y = rnd((400, D), seed + 100)
+        x[:, 0] += 2.0
+        y[:, 0] += 2.0
+        xn = x / np.linalg.norm(x, axis=-1, keepdims=True)
+        yn = y / np.linalg.norm(y, axis=-1, keepdims=True)
+        s32 = xn.astype(np.float32) @ yn.astype(np.float32).T
+        assert np.max(np.abs(s32.astype(np.float64) - xn @ yn.T)) < 0.1 * O.SCREEN_MARGIN
+
+
+@pytest.mark.parametrize("causal,Tq,Tk,kpm,drop", [
+    (True, 96, 96, False, None), (True, 130, 70, True, None), (True, 50, 120, False, (0.3, 99)),
+    (False, 80, 140, True, None), (False, 64, 64, False, (0.5, 7))])
+def test_sparse_forward_backward_matches_dense(causal, Tq, Tk, kpm, drop):
+    B, H, D = 2, 3, 32
+    q, k, v = rnd((B, Tq, H, D), 50), rnd((B, Tk, H, D), 51), rnd((B, Tk, H, D), 52)
+    q[..., :2] += 0.8
+    k[..., :2] += 0.8
+    dy = rnd((B, Tq, H, D), 53)
+    r, w = np.array([1.1, 1.3, 1.9]), np.array([7.5, 40.0, 1e5])
+    mask = None
+    if kpm:
+        mask = np.zeros((B, Tk), dtype=bool)
+        mask[0, 5:9] = True
+        mask[1, -1] = True
+    y, grads, P = O.sparse_forward_backward(q, k, v, r, w, dy, causal, key_padding_mask=mask, dropout=drop)
+    assert len(P["i"]) > 200
+    yd = O.forward(q, k, v, r, w, causal, key_padding_mask=mask, dropout=drop)
+    gd = O.backward(q, k, v, r, w, dy, causal, key_padding_mask=mask, dropout=drop)
+    assert np.max(np.abs(yd)) > 1e-2
+    np.testing.assert_allclose(y, yd, rtol=0, atol=1e-12)
+    for name, a, b in zip(("dq", "dk", "dv", "dr", "dw"), grads, gd):
+        assert np.max(np.abs(b)) > 1e-4, name
+        np.testing.assert_allclose(a, b, rtol=0, atol=1e-11 * max(1.0, np.max(np.abs(b)))), name
