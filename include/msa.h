@@ -152,12 +152,16 @@ size_t msa_decode_workspace_bytes(int B, int H, int D, int max_len);
  *   q      : (B, H, D) raw query projection, strides (q_sb, q_sh), unit D.
  *   kcache, vcache : (B, Tcap, H, D) raw k/v projections, strides (sb, st, sh);
  *            cache_cap = Tcap, and 1 <= cache_len <= cache_cap.
+ *   window_hint : 0, or a bound on ceil(w_h) over the heads that sizes the
+ *            launch (one block per 2048-key chunk of each window).  Only the
+ *            windowed keys are visited whatever its value; a wrong hint costs
+ *            time, never correctness.
  *   y      : (B, H, D) contiguous, TanhNorm(h).
  */
 int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
                const void* kcache, int64_t k_sb, int64_t k_st, int64_t k_sh,
                const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh,
-               int B, int H, int D, int dtype, int cache_len, int cache_cap,
+               int B, int H, int D, int dtype, int cache_len, int cache_cap, int window_hint,
                const float* r, const float* w, float eps,
                void* y, void* workspace, size_t workspace_bytes, void* stream);
 

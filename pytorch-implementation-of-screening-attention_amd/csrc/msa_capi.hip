@@ -288,14 +288,16 @@ size_t msa_decode_workspace_bytes(int B, int H, int D, int max_len) {
   return (size_t)B * H * msa::decode_max_chunks(max_len) * D * sizeof(float);
 }
 
-int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
-               int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int D,
-               int dtype, int cache_len, int cache_cap, const float* r, const float* w, float eps, void* y,
-               void* workspace, size_t workspace_bytes, void* stream) {
+// Validates a decode call and fills c (all but the partial-sum buffer).
+// Returns MSA_OK, an error code, or -1 when B == 0 (nothing to do).
+static int decode_setup(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
+                        int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H,
+                        int D, int dtype, int cache_len, int cache_cap, int window_hint, const float* r,
+                        const float* w, float eps, void* y, void* stream, msa::DecodeCall* c) {
   msa::Geometry g;
   int rc = check_geometry(B, H, 1, cache_len, D, dtype, 1, &g);
   if (rc != MSA_OK) return rc;
-  if (B == 0) return ok();
+  if (B == 0) return -1;
   if (cache_len <= 0) return fail(MSA_ERR_INVALID, "cache_len must be >= 1 (the new token is in the cache)");
   if (cache_len > cache_cap)
     return fail(MSA_ERR_INVALID, "cache_len %d exceeds the cache capacity %d", cache_len, cache_cap);
@@ -305,19 +307,33 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, in
   if ((rc = check_tensor("vcache", vcache, v_sb, v_st, v_sh, dtype)) != MSA_OK) return rc;
   if (r == nullptr || w == nullptr) return fail(MSA_ERR_INVALID, "r and w must be device arrays of H floats");
   if ((rc = check_out("y", y)) != MSA_OK) return rc;
+  c->B = B; c->H = H; c->D = D; c->DP = g.DP; c->dtype = dtype; c->len = cache_len;
+  c->q = q; c->q_sb = q_sb; c->q_sh = q_sh;
+  c->kc = kcache; c->ks = {k_sb, k_st, k_sh};
+  c->vc = vcache; c->vs = {v_sb, v_st, v_sh};
+  c->r = r; c->w = w; c->eps = eps;
+  c->y = y; c->part = nullptr;
+  // one block per window chunk of every head when the hint bounds the
+  // windows; any grid gives the same result, the hint only sizes it
+  const int span = window_hint > 0 && window_hint < cache_len ? window_hint : cache_len;
+  c->blocks = B * H * msa::decode_max_chunks(span);
+  c->stream = (hipStream_t)stream;
+  return MSA_OK;
+}
+
+int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
+               int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int D,
+               int dtype, int cache_len, int cache_cap, int window_hint, const float* r, const float* w, float eps,
+               void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  msa::DecodeCall c;
+  const int rc = decode_setup(q, q_sb, q_sh, kcache, k_sb, k_st, k_sh, vcache, v_sb, v_st, v_sh, B, H, D, dtype,
+                              cache_len, cache_cap, window_hint, r, w, eps, y, stream, &c);
+  if (rc == -1) return ok();
+  if (rc != MSA_OK) return rc;
   const size_t need = msa_decode_workspace_bytes(B, H, D, cache_len);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(MSA_ERR_WORKSPACE, "decode workspace holds %zu bytes, %zu needed", workspace_bytes, need);
-  msa::DecodeCall c;
-  c.B = B; c.H = H; c.D = D; c.DP = g.DP; c.dtype = dtype; c.len = cache_len;
-  c.q = q; c.q_sb = q_sb; c.q_sh = q_sh;
-  c.kc = kcache; c.ks = {k_sb, k_st, k_sh};
-  c.vc = vcache; c.vs = {v_sb, v_st, v_sh};
-  c.r = r; c.w = w; c.eps = eps;
-  c.y = y; c.part = (float*)workspace;
-  c.nchunks = msa::decode_max_chunks(cache_len);
-  c.chunk = msa::decode_chunk_keys();
-  c.stream = (hipStream_t)stream;
+  c.part = (float*)workspace;
   return hip_status(msa::launch_decode(c), "msa_decode launch");
 }
 

@@ -1,13 +1,17 @@
 // Single-query decode against a KV cache (gfx950).
 //
 // The query at position pos = len-1 attends to keys j in (pos - w, pos]
-// (causal window, attention.py:111-118).  The window is split into chunks of
-// kChunk keys; each 256-thread block streams one chunk of raw K rows
-// (16-byte loads, D/VEC lanes per key), forms s = q.k/(|q||k|) from exact
-// products of the raw values on the fly,
-// and reads a V row only when its alpha*m is non-zero.  Because screening has
-// no softmax normaliser (attention.py:192-193), chunk partials simply add; a
-// second kernel sums them in a fixed order and applies TanhNorm (norm.py:23-25).
+// (causal window, attention.py:111-118).  Each head's window is cut into
+// chunks of kChunk keys; a work item is one (b, h, chunk), items numbered in
+// (b, h, chunk) order, and the number of items is computed on the device from
+// the windows themselves, so only windowed keys are ever visited.  Blocks of
+// 256 threads take items blockIdx.x, blockIdx.x + gridDim.x, ...; for each
+// they stream the chunk's raw K rows (16-byte loads, D/VEC lanes per key),
+// form s = q.k/(|q||k|) from exact products of the raw values, and read a V
+// row only when its alpha*m is non-zero.  Because screening has no softmax
+// normaliser (attention.py:192-193), chunk partials simply add: a second
+// kernel sums each head's partials in a fixed order and applies TanhNorm
+// (norm.py:23-25).  Results do not depend on the grid size.
 #include <type_traits>
 
 #include "msa_device.h"
@@ -23,9 +27,9 @@ struct DecArgs {
   const void* kc; Strides3 ks;
   const void* vc; Strides3 vs;
   const float* r; const float* w;
-  float* part;  // [B*H][nchunks][D]
+  float* part;  // [item][D], items in (b, h, chunk) order
   void* y;
-  int H, len, nchunks;
+  int B, H, len;
   float eps;
 };
 
@@ -64,6 +68,57 @@ __device__ inline float group_sum(float x) {
   return x;
 }
 
+// First key of head h's window at position pos, and its number of chunks.
+__device__ inline int64_t window_lo(const DecArgs& a, int h) {
+  const HeadParams hp = head_params(a.r, a.w, h, true);
+  const int64_t lo = (int64_t)a.len - hp.wc;  // pos - wc + 1
+  return lo < 0 ? 0 : lo;
+}
+__device__ inline int head_chunks(const DecArgs& a, int h) {
+  return (int)(((int64_t)a.len - window_lo(a, h) + kChunk - 1) / kChunk);
+}
+
+// Wave-uniform item map (every lane of the wave calls these).  Per batch row
+// the items are the heads' chunks in head order.  items_per_b(): the count;
+// head_of(rem, h, c0): the head h whose items hold index rem of a batch row,
+// and the index c0 of that head's first item.
+__device__ inline int lane_inclusive_scan(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+__device__ inline int items_per_b(const DecArgs& a) {
+  const int lane = threadIdx.x & 63;
+  int total = 0;
+  for (int h0 = 0; h0 < a.H; h0 += 64) {
+    const int c = h0 + lane < a.H ? head_chunks(a, h0 + lane) : 0;
+    total += __shfl(lane_inclusive_scan(c), 63);
+  }
+  return total;
+}
+__device__ inline void head_of(const DecArgs& a, int rem, int& h, int& c0) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  for (int h0 = 0; h0 < a.H; h0 += 64) {
+    const int c = h0 + lane < a.H ? head_chunks(a, h0 + lane) : 0;
+    const int incl = lane_inclusive_scan(c) + carry;
+    const unsigned long long sel = __ballot(h0 + lane < a.H && incl > rem);
+    if (sel != 0ull) {
+      const int l = (int)__builtin_ctzll(sel);
+      h = h0 + l;
+      c0 = __shfl(incl - c, l);
+      return;
+    }
+    carry = __shfl(incl, 63);
+  }
+  h = a.H - 1;  // not reached for rem < items_per_b
+  c0 = carry;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
   using V = Vec16<T>;
@@ -73,21 +128,24 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
   constexpr int KPW = kWave / LPK;          // keys per wave per load
   __shared__ float red[4][D];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const HeadParams hp = head_params(a.r, a.w, h, true);
-  const int64_t pos = a.len - 1;
-  int64_t lo = pos - hp.wc + 1;
-  if (lo < 0) lo = 0;
-  const int64_t n = pos - lo + 1;
-  const int64_t c0 = lo + (int64_t)blockIdx.x * kChunk;
   const int sub = lane % LPK, kl = lane / LPK;
   const int d0 = sub * VEC;
+  const int64_t pos = a.len - 1;
+  const int per_b = items_per_b(a);
+  const int total = a.B * per_b;
 
-  float acc[VEC];
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const int b = item / per_b;
+    int h, c0i;
+    head_of(a, item - b * per_b, h, c0i);
+    const int chunk = item - b * per_b - c0i;
+    const HeadParams hp = head_params(a.r, a.w, h, true);
+    const int64_t c0 = window_lo(a, h) + (int64_t)chunk * kChunk;
+    const int64_t cend = c0 + kChunk < pos + 1 ? c0 + kChunk : pos + 1;
+
+    float acc[VEC];
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
-
-  if ((int64_t)blockIdx.x * kChunk < n) {
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
     // raw query slice and 1/|q| (each LPK-lane group covers the whole row);
     // s = (q . k) / (|q| |k|) with exact products of the raw values
     const vec qv = *reinterpret_cast<const vec*>((const T*)a.q + b * a.q_sb + h * a.q_sh + d0);
@@ -95,7 +153,6 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
 #pragma unroll
     for (int o = 1; o < LPK; o <<= 1) qq += __shfl_xor(qq, o);
     const float iq = 1.0f / fmaxf(sqrtf(qq), a.eps);
-    const int64_t cend = c0 + kChunk < pos + 1 ? c0 + kChunk : pos + 1;
     const T* kb = (const T*)a.kc + b * a.ks.sb + h * a.ks.sh + d0;
     const T* vb = (const T*)a.vc + b * a.vs.sb + h * a.vs.sh + d0;
     for (int64_t base = c0 + (int64_t)wave * KPW * kDecUnroll; base < cend; base += 4 * KPW * kDecUnroll) {
@@ -124,36 +181,51 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
         }
       }
     }
-  }
-  // reduce over the key groups of the wave, then over the 4 waves
+    // reduce over the key groups of the wave, then over the 4 waves
 #pragma unroll
-  for (int o = LPK; o < kWave; o <<= 1)
+    for (int o = LPK; o < kWave; o <<= 1)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], o);
-  if (kl == 0)
+      for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], o);
+    if (kl == 0)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) red[wave][d0 + e] = acc[e];
-  __syncthreads();
-  if (threadIdx.x < D) {
-    const int d = threadIdx.x;
-    a.part[((int64_t)bh * a.nchunks + blockIdx.x) * D + d] = red[0][d] + red[1][d] + red[2][d] + red[3][d];
+      for (int e = 0; e < VEC; ++e) red[wave][d0 + e] = acc[e];
+    __syncthreads();
+    if (threadIdx.x < D) {
+      const int d = threadIdx.x;
+      a.part[(int64_t)item * D + d] = red[0][d] + red[1][d] + red[2][d] + red[3][d];
+    }
+    __syncthreads();  // red is reused by the next item
   }
 }
 
-// Sum of the chunk partials in a fixed order (chunk groups c % G, then the
-// groups in order) and TanhNorm; block per (b, h).
+// Sum of head (b, h)'s chunk partials in a fixed order (chunk groups c % G,
+// then the groups in order) and TanhNorm; block per (b, h).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecArgs a) {
   constexpr int G = 256 / D;  // chunk groups
   __shared__ float red[256];
   __shared__ float sq[D];
+  __shared__ int map[2];  // first item of head (b, h), its number of items
   const int bh = blockIdx.x, t = threadIdx.x, d = t % D, g = t / D;
-  const HeadParams hp = head_params(a.r, a.w, bh % a.H, true);
-  const int64_t pos = a.len - 1;
-  int64_t lo = pos - hp.wc + 1;
-  if (lo < 0) lo = 0;
-  const int used = (int)((pos - lo + 1 + kChunk - 1) / kChunk);
-  const float* pp = a.part + (int64_t)bh * a.nchunks * D + d;
+  const int b = bh / a.H, hh = bh % a.H;
+  if (t < 64) {  // wave 0 maps the items; the block shares the result
+    const int per_b = items_per_b(a);
+    int carry = 0, first = 0;
+    for (int h0 = 0; h0 < a.H; h0 += 64) {
+      const int c = h0 + t < a.H ? head_chunks(a, h0 + t) : 0;
+      const int incl = lane_inclusive_scan(c) + carry;
+      const int excl = __shfl(incl - c, (hh - h0) & 63);  // items of heads before hh
+      if (hh >= h0 && hh < h0 + 64) first = excl;
+      carry = __shfl(incl, 63);
+    }
+    if (t == 0) {
+      map[0] = b * per_b + first;
+      map[1] = head_chunks(a, hh);
+    }
+  }
+  __syncthreads();
+  const int used = map[1];
+  const float* pp = a.part + d + (int64_t)map[0] * D;
   float x0 = 0.0f, x1 = 0.0f;
   int c = g;
   for (; c + G < used; c += 2 * G) {
@@ -188,11 +260,10 @@ static hipError_t launch_decode_t(const DecodeCall& c) {
   a.q = c.q; a.q_sb = c.q_sb; a.q_sh = c.q_sh;
   a.kc = c.kc; a.ks = c.ks; a.vc = c.vc; a.vs = c.vs;
   a.r = c.r; a.w = c.w; a.part = c.part; a.y = c.y;
-  a.H = c.H; a.len = c.len; a.nchunks = c.nchunks; a.eps = c.eps;
+  a.B = c.B; a.H = c.H; a.len = c.len; a.eps = c.eps;
   // the decode timer brackets both kernels: the whole single-query step
   timer_begin(7, c.stream);
-  hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3((unsigned)c.nchunks, (unsigned)(c.B * c.H)), dim3(256), 0,
-                     c.stream, a);
+  hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3((unsigned)c.blocks), dim3(256), 0, c.stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((decode_reduce_kernel<T, D>), dim3((unsigned)(c.B * c.H)), dim3(256), 0, c.stream, a);

@@ -91,10 +91,13 @@ struct DecodeCall {
   const void* kc; Strides3 ks;
   const void* vc; Strides3 vs;
   const float* r; const float* w; float eps;
-  void* y; float* part; int nchunks; int chunk;
+  void* y; float* part;
+  int blocks;  // grid size of the partial-sum kernel (any value >= 1 gives the same result)
   hipStream_t stream;
 };
 int decode_chunk_keys();
+// Chunks of a head's window at most, ceil(max_len / chunk): the decode
+// workspace holds B*H of them, D floats each.
 int decode_max_chunks(int max_len);
 hipError_t launch_decode(const DecodeCall& c);
 

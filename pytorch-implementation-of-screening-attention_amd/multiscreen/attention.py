@@ -134,7 +134,7 @@ class ScreeningAttention(nn.Module):
         if x.is_cuda:
             # the cache's dtype is the kernel's (fp16 models keep an fp32 cache)
             y = ops.decode_step(q[:, 0].to(cache.k.dtype), cache.k, cache.v, pos + 1, r, w, self.eps,
-                                cache.workspace).to(x.dtype)
+                                cache.workspace, cache.window_hint).to(x.dtype)
         else:
             y = screening_core_dense(q, kc, vc, r, w, True, self.eps, q_offset=pos)[:, 0]
         return self.out_proj(y.reshape(B, 1, self.d_model))
@@ -148,9 +148,12 @@ class KVCache:
     H, D) views of that storage, the layout of the projections.  The kernels
     compute in float32 or bfloat16, so a float16 model's cache is float32."""
 
-    def __init__(self, batch, capacity, num_heads, head_dim, dtype, device):
+    def __init__(self, batch, capacity, num_heads, head_dim, dtype, device, window_hint=0):
         if dtype == torch.float16:
             dtype = torch.float32
+        # 0, or a bound on ceil(w) over the layer's heads: sizes the decode
+        # launch to the windows instead of the cache (results do not depend on it)
+        self.window_hint = int(window_hint)
         self._k = torch.zeros((batch, num_heads, capacity, head_dim), dtype=dtype, device=device)
         self._v = torch.zeros_like(self._k)
         self.k = self._k.permute(0, 2, 1, 3)

@@ -13,6 +13,8 @@ then runs one single-query decode step per token (the HIP decode kernel on
 GPU), which computes the same last-position logits.
 """
 
+import math
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -74,9 +76,17 @@ class MultiscreenLM(nn.Module):
         return result
 
     def new_cache(self, batch: int, capacity: int, dtype: torch.dtype, device) -> list:
-        attn = self.blocks[0].attn
-        return [KVCache(batch, capacity, attn.num_heads, attn.head_dim, dtype, device)
-                for _ in self.blocks]
+        """One KVCache per block.  Each carries its layer's widest window
+        (ceil(max_h w_h), read once here) so that decode launches only the
+        blocks the windows need."""
+        caches = []
+        for block in self.blocks:
+            attn = block.attn
+            with torch.no_grad():
+                wmax = float(attn.window().max())
+            hint = min(capacity, math.ceil(wmax)) if math.isfinite(wmax) else 0
+            caches.append(KVCache(batch, capacity, attn.num_heads, attn.head_dim, dtype, device, hint))
+        return caches
 
     def _head(self, x: torch.Tensor) -> torch.Tensor:
         return self.lm_head(self.norm(x))

@@ -171,11 +171,12 @@ def screening_core(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, 
     return ScreeningCoreFunction.apply(q, k, v, r, w, causal, eps, key_padding_mask, dropout_p, seed)
 
 
-def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None):
+def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None, window_hint=0):
     """Screening attention of one new query per (b, h) against a KV cache.
 
     q (B, H, D); kcache/vcache (B, Tcap, H, D) holding the raw k/v projections
     of positions [0, cache_len), the last being the query's own token.
+    window_hint: 0, or a bound on ceil(w) over the heads (sizes the launch only).
     Returns y (B, H, D) = TanhNorm(h) of that token.
     """
     L = _native.lib()
@@ -201,7 +202,8 @@ def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None):
         raise ValueError(f"cache shapes {tuple(kcache.shape)}/{tuple(vcache.shape)} do not match q {tuple(q.shape)}")
     rc = L.msa_decode(q.data_ptr(), q.stride(0), q.stride(1),
                       *_args_bthd(kcache), *_args_bthd(vcache),
-                      B, H, D, dt, int(cache_len), int(kcache.shape[1]), r32.data_ptr(), w32.data_ptr(),
+                      B, H, D, dt, int(cache_len), int(kcache.shape[1]), int(window_hint),
+                      r32.data_ptr(), w32.data_ptr(),
                       float(eps),
                       y.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
                       _stream_ptr(dev))

@@ -100,13 +100,13 @@ def test_bwd_and_decode_reject_bad_arguments():
     rc = L.msa_bwd(16, 8, 8, 8, 16, 8, 8, 8, 16, 8, 8, 8, 1, 1, 8, 8, 16, 1, 16, 16, None, 1, 1e-8, 0.0, 0,
                    16, 16, 16, 16, 0, 16, 16, 16, 16, 16, 16, 1 << 20, None)
     assert rc == 2 and "tile_bits" in L.msa_last_error().decode()
-    rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 0, 100, 16, 16,
+    rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 0, 100, 0, 16, 16,
                       1e-8, 16, 16, 1 << 30, None)
     assert rc == 1 and "cache_len" in L.msa_last_error().decode()
-    rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 101, 100, 16, 16,
+    rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 101, 100, 0, 16, 16,
                       1e-8, 16, 16, 1 << 30, None)
     assert rc == 1 and "capacity" in L.msa_last_error().decode()
-    rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 10, 100, 16, 16,
+    rc = L.msa_decode(16, 512, 64, 16, 512, 512, 64, 16, 512, 512, 64, 1, 8, 64, 1, 10, 100, 0, 16, 16,
                       1e-8, 16, 16, 8, None)
     assert rc == 2 and "decode workspace" in L.msa_last_error().decode()
 

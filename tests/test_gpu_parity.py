@@ -321,6 +321,27 @@ def test_decode_matches_forward_rows(dtype):
         assert rel_err(np64(y), yfull[:, L - 1]) <= TOL[dtype], L
 
 
+def test_decode_window_hint_changes_only_the_grid():
+    # the hint sizes the launch; too small, exact, too large or absent, the
+    # output is bitwise the same and matches the oracle.  H = 72 takes the
+    # head scan over more than one wave of lanes.
+    B, T, H, D = 2, 5000, 72, 16
+    q, k, v = correlated_qkv(B, T, T, H, D, seed=13, dtype=torch.bfloat16, rho=0.35)
+    g = torch.Generator().manual_seed(3)
+    r = (1.1 + 0.3 * torch.rand(H, generator=g)).tolist()
+    w = (2.0 + 6000.0 * torch.rand(H, generator=g) ** 3).tolist()
+    ops = _ops()
+    rg, wg = _rw(H, r, w)
+    kc, vc = k.to(DEV), v.to(DEV)
+    for L in (1, 2049, 5000):
+        qd = q[:, L - 1].to(DEV)
+        base = ops.decode_step(qd, kc, vc, L, rg, wg)
+        for hint in (1, 2048, math.ceil(max(w)), 10 ** 6):
+            assert torch.equal(ops.decode_step(qd, kc, vc, L, rg, wg, window_hint=hint), base), (L, hint)
+        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, np.array(r), np.array(w))
+        assert rel_err(np64(base), ref) <= 2e-2, L
+
+
 @pytest.mark.parametrize("name", GOLDEN_ATTENTION)
 def test_module_matches_reference_golden_fp32(name):
     from multiscreen import ScreeningAttention
