@@ -165,6 +165,26 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
                const float* r, const float* w, float eps,
                void* y, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * msa_decode without a workspace argument and without any allocation: the
+ * split-key partial sums go to a static device array of
+ * MSA_DECODE_STATIC_SCRATCH_BYTES per GPU, held until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, checks and results as msa_decode; it
+ * fails with MSA_ERR_WORKSPACE when msa_decode_workspace_bytes(B, H, D,
+ * cache_len) exceeds the array (B*H*ceil(cache_len/2048)*D*4 bytes: e.g.
+ * B*H = 128 heads of D = 64 up to cache_len 1,048,576).  Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (several streams
+ * or threads) race; calls ordered on one stream do not.
+ */
+#define MSA_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
+int msa_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                       const void* kcache, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                       const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                       int B, int H, int D, int dtype, int cache_len, int cache_cap, int window_hint,
+                       const float* r, const float* w, float eps, void* y, void* stream);
+
 /* Kernel timing for measurement.  After msa_timer_arm(kernel, n) the next n
  * launches of that kernel (any entry point) each record a HIP event pair on
  * their stream around the launch; several kernels can be armed at once.

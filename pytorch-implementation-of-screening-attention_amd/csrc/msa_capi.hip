@@ -337,6 +337,66 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, in
   return hip_status(msa::launch_decode(c), "msa_decode launch");
 }
 
+// ---------------------------------------------------------------------------
+// Decode without allocation.  The partial sums live in `scratch`, a static
+// device array: every GPU the library runs on holds its own copy (16 MiB)
+// until the process ends.  Host code never uses the array's name as an
+// address: on the first call on each device, with that device current, its
+// device address is looked up once and kept per device.  Calls that overlap
+// on one GPU share the array and race; nothing in it needs clearing (every
+// partial is written before it is read).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[MSA_DECODE_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+struct ScratchTable {
+  std::mutex mu;
+  std::vector<void*> ptr;  // device address of `scratch`, per device ordinal
+};
+ScratchTable& scratch_table() {
+  static ScratchTable t;
+  return t;
+}
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MSA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  ScratchTable& t = scratch_table();
+  std::lock_guard<std::mutex> g(t.mu);
+  if (dev >= (int)t.ptr.size()) t.ptr.resize(dev + 1, nullptr);
+  if (t.ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(MSA_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    t.ptr[dev] = p;
+  }
+  *out = t.ptr[dev];
+  return MSA_OK;
+}
+}  // namespace
+
+int msa_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
+                       int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H,
+                       int D, int dtype, int cache_len, int cache_cap, int window_hint, const float* r,
+                       const float* w, float eps, void* y, void* stream) {
+  msa::DecodeCall c;
+  int rc = decode_setup(q, q_sb, q_sh, kcache, k_sb, k_st, k_sh, vcache, v_sb, v_st, v_sh, B, H, D, dtype,
+                        cache_len, cache_cap, window_hint, r, w, eps, y, stream, &c);
+  if (rc == -1) return ok();
+  if (rc != MSA_OK) return rc;
+  const size_t need = msa_decode_workspace_bytes(B, H, D, cache_len);
+  if (need > (size_t)MSA_DECODE_STATIC_SCRATCH_BYTES)
+    return fail(MSA_ERR_WORKSPACE,
+                "msa_decode_noalloc: %zu bytes of partial sums needed (B*H*ceil(cache_len/2048)*D*4), the static "
+                "scratch holds %zu; use msa_decode with a workspace",
+                need, (size_t)MSA_DECODE_STATIC_SCRATCH_BYTES);
+  void* p = nullptr;
+  if ((rc = scratch_address(&p)) != MSA_OK) return rc;
+  c.part = (float*)p;
+  return hip_status(msa::launch_decode(c), "msa_decode_noalloc launch");
+}
+
 int msa_selftest_mfma(const float* a16, const float* b16, float* out16, const float* a2, const float* b2,
                       float* out2, void* stream) {
   if (!a16 || !b16 || !out16 || !a2 || !b2 || !out2) return fail(MSA_ERR_INVALID, "null pointer");
