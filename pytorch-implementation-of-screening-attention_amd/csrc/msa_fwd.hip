@@ -3,6 +3,7 @@
 //   prep_k_kernel : unit-normalised K^ rows (attention.py:156-157) in a padded
 //                   [b*h][Tk_pad][DP] buffer; key padding (attention.py:185-188)
 //                   is folded in as a zero row (s = 0 gives alpha = 0: r > 1).
+//                   Its first row of blocks plans the screen's work (below).
 //   fwd_screen_kernel : 256-thread block = 4 waves, wave -> one 64-query tile
 //                   of one head.  Key tiles of the block's window are copied
 //                   global -> LDS by direct DMA into a 4-slot ring (3 tiles in
@@ -23,16 +24,248 @@
 
 namespace msa {
 
+// ---------------------------------------------------------------------------
+// Screen work plan.  The hardware places the blocks of a launch statically:
+// block p runs on XCD p % 8 and, within that XCD, on shader engine
+// perm[(p >> 3) % 4] (a fixed permutation per XCD, measured on MI355X with
+// per-block hardware-id stamps); only the choice among the engine's 8 CUs is
+// dynamic.  So a launch is 32 "lanes" (XCD, engine) of 8 CUs, each taking
+// its blocks in order, and the screen's makespan is set by the busiest lane
+// and by its longest block.  The plan cuts each 4-query-tile group's
+// key-tile range into items of at most `seg` tiles, near-equal in length,
+// sorts items longest first and deals them over lanes in boustrophedon
+// order, so every lane gets an equal share and runs its longest items first:
+//   per-XCD mode (B*H >= 32): heads are dealt to XCDs widest window first in
+//     boustrophedon order and stay there (a head's K^ stays in one L2); each
+//     XCD's items are dealt over its 4 engine lanes;
+//   global mode (fewer heads, where one XCD per head would leave XCDs idle or
+//     overloaded): all items are dealt over all 32 lanes.
+// Screen block p takes entry (p % 8, (p >> 3) % 4, p >> 5) of the table;
+// positions past a lane's items hold bh = -1 (the block exits at once).
+// Which items run where changes only the time, never the bitmap (live bits
+// are ORed).
+// ---------------------------------------------------------------------------
+struct ScreenItem {
+  int bh, grp, lo, hi;  // head, 4-query-tile group, key tiles [lo, hi]
+};
+struct ScreenPlan {
+  ScreenItem* table;  // [8 XCDs][4 engine lanes][kmax]
+  int kmax;           // positions per lane
+  int seg;            // key tiles per item at most (<= 256)
+  int per_xcd;        // 1: per-XCD mode, 0: global mode
+};
+
 struct PrepKArgs {
   const void* k; Strides3 ks;
   const uint8_t* kpm;
   void* khat;
   uint32_t* bits;
   int64_t bits_per_bh;  // bitmap words per (b, h)
-  int H, Tk, D;
+  int B, H, Tq, Tk, D, nqt, causal;
   int64_t Tk_pad;
   float eps;
+  const float* r; const float* w;
+  ScreenPlan plan;
 };
+
+// Key tiles [lo, hi] holding the window of queries [qa, qb] (empty: hi < lo).
+__device__ inline void window_tiles(int Tk, const HeadParams& hp, bool causal, int64_t qa, int64_t qb, int& lo,
+                                    int& hi) {
+  int64_t jlo = qa - hp.wc + 1;
+  int64_t jhi = causal ? qb : qb + hp.wc - 1;
+  if (jlo < 0) jlo = 0;
+  if (jhi > Tk - 1) jhi = Tk - 1;
+  lo = (int)(jlo / kTile);
+  hi = jhi >= jlo ? (int)(jhi / kTile) : lo - 1;
+}
+
+// Per-XCD mode: the heads of XCD x.  Heads are ranked widest window first
+// (NaN keyed as widest, ties by index: a permutation); rank k goes to XCD
+// (k/8 odd ? 7 - k%8 : k%8) as its (k/8)-th head.  Above kPlanMaxRanked heads
+// the ranking is skipped: slot jh of XCD x is head 8*jh + x.
+constexpr int kPlanMaxRanked = 512;
+constexpr int kPlanMaxHeads = 512;  // head slots a planner block keeps in LDS
+__device__ inline int xcd_head_count(int BH, int x) {
+  int nh = 0;
+  for (int jh = 0; 8 * jh < BH; ++jh) nh += 8 * jh + ((jh & 1) ? 7 - x : x) < BH ? 1 : 0;
+  return nh;
+}
+// keys[h] (the window ranking key of head h) are in LDS when B*H <= kPlanMaxRanked.
+__device__ inline void plan_heads(const PrepKArgs& a, int x, int* heads, const float* keys) {
+  const int BH = a.B * a.H;
+  if (BH > kPlanMaxRanked) {
+    for (int jh = threadIdx.x; 8 * jh < BH && jh < kPlanMaxHeads; jh += blockDim.x)
+      if (8 * jh + x < BH) heads[jh] = 8 * jh + x;
+    return;
+  }
+  for (int bh = threadIdx.x; bh < BH; bh += blockDim.x) {
+    const float key = keys[bh % a.H];
+    int rank = 0;
+    for (int o = 0, ho = 0; o < BH; ++o) {
+      const float ko = keys[ho];
+      rank += (ko > key || (ko == key && o < bh)) ? 1 : 0;
+      ho = ho + 1 == a.H ? 0 : ho + 1;
+    }
+    const int jh = rank >> 3, xr = (jh & 1) ? 7 - (rank & 7) : (rank & 7);
+    if (xr == x) heads[jh] = bh;
+  }
+}
+
+// Integer window as head_params forms it.
+__device__ inline int plan_wc(float w) {
+  const float c = ceilf(w);
+  return !(c > 0.0f) ? 0 : (c > 1073741824.0f ? 1073741824 : (int)c);
+}
+
+// Visits the planned items: fn(bh, grp, lo, hi) for each (head slot, group)
+// pair's near-equal cut of its key-tile range into ceil(steps / seg) items.
+// heads[slot] and the integer windows wcs[slot] are in LDS for the first
+// kPlanMaxHeads slots; beyond them (per-XCD mode without ranking only) slot
+// jh is head 8*jh + x.
+template <typename Fn>
+__device__ inline void plan_items(const PrepKArgs& a, int x, const int* heads, const int* wcs, int nh, Fn&& fn) {
+  const int ngroups = (a.nqt + 3) / 4;
+  const bool causal = a.causal != 0;
+  const int seg = a.plan.seg;
+  for (int idx = threadIdx.x; idx < nh * ngroups; idx += blockDim.x) {
+    const int slot = idx / ngroups, grp = idx - slot * ngroups;
+    const bool cached = slot < kPlanMaxHeads;
+    const int bh = cached ? heads[slot] : 8 * slot + x;
+    const int wc = cached ? wcs[slot] : plan_wc(a.w[bh % a.H]);
+    {
+      const int qa = grp * 4 * kTile, qb = qa + 4 * kTile - 1 < a.Tq - 1 ? qa + 4 * kTile - 1 : a.Tq - 1;
+      int jlo = qa - wc + 1;                  // wc <= 2^30 and positions < 2^22: no overflow
+      int jhi = causal ? qb : (wc - 1 > a.Tk ? a.Tk : qb + wc - 1);
+      if (jlo < 0) jlo = 0;
+      if (jhi > a.Tk - 1) jhi = a.Tk - 1;
+      if (jhi < jlo) continue;
+      const int lo = jlo / kTile, steps = jhi / kTile - lo + 1;
+      const int n = (steps + seg - 1) / seg, base = steps / n, rem = steps - base * n;
+      for (int i = 0, s0 = lo; i < n; ++i) {
+        const int len = base + (i < rem ? 1 : 0);
+        fn(bh, grp, s0, s0 + len - 1);
+        s0 += len;
+      }
+    }
+  }
+}
+
+// Boustrophedon deal of sorted position i over nl lanes: (lane, slot).
+__device__ inline void plan_deal(int i, int nl, int& e, int& j) {
+  j = i / nl;
+  const int r = i - j * nl;
+  e = (j & 1) ? nl - 1 - r : r;
+}
+
+// Planner block x (256 threads).  Per-XCD mode: block x writes the 4 lanes
+// of XCD x.  Global mode: block 0 writes all 32 lanes (lane L = XCD L % 8,
+// engine L / 8).
+__device__ void screen_plan(const PrepKArgs& a, int x) {
+  __shared__ int heads[kPlanMaxHeads], wcs[kPlanMaxHeads];
+  __shared__ float keys[kPlanMaxRanked];
+  __shared__ int wch[kPlanMaxRanked];
+  __shared__ int hist[257], start[257];
+  __shared__ int total;
+  const bool per_xcd = a.plan.per_xcd != 0;
+  if (!per_xcd && x != 0) return;
+  const int t = threadIdx.x, nl = per_xcd ? 4 : 32, kmax = a.plan.kmax;
+  for (int i = t; i < 257; i += blockDim.x) hist[i] = 0;
+  const int BH = a.B * a.H;
+  const int nh = per_xcd ? xcd_head_count(BH, x) : BH;  // global mode: BH < 32
+  // the one global read of the windows (the planner runs beside prep_k's
+  // stream, where every dependent memory round trip is slow)
+  const bool small_h = a.H <= kPlanMaxRanked;
+  if (small_h)
+    for (int h = t; h < a.H; h += blockDim.x) {
+      const float wf = a.w[h];
+      keys[h] = window_rank_key(wf);
+      wch[h] = plan_wc(wf);
+    }
+  __syncthreads();
+  if (per_xcd) {
+    plan_heads(a, x, heads, keys);
+  } else {
+    for (int i = t; i < nh; i += blockDim.x) heads[i] = i;
+  }
+  __syncthreads();
+  for (int i = t; i < nh && i < kPlanMaxHeads; i += blockDim.x) {
+    const int h = heads[i] % a.H;
+    wcs[i] = small_h ? wch[h] : plan_wc(a.w[h]);
+  }
+  __syncthreads();
+  // items by length (at most seg <= 256), longest first; the order among
+  // items of one length is whatever the atomics give (it only moves time)
+  plan_items(a, x, heads, wcs, nh, [&](int, int, int lo, int hi) { atomicAdd(&hist[hi - lo + 1], 1); });
+  __syncthreads();
+  if (t < 64) {  // exclusive prefix over lengths 256 .. 1: lane t holds 256-4t .. 253-4t
+    int v[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[k] = hist[256 - 4 * t - k];
+      sum += v[k];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (t >= o) incl += y;
+    }
+    int acc = incl - sum;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      start[256 - 4 * t - k] = acc;
+      acc += v[k];
+    }
+    if (t == 63) total = incl;
+  }
+  __syncthreads();
+  // lane e of this planner -> table lane (XCD, engine)
+  auto lane_base = [&](int e) -> ScreenItem* {
+    const int xcd = per_xcd ? x : e % 8, eng = per_xcd ? e : e / 8;
+    return a.plan.table + (xcd * 4 + eng) * kmax;
+  };
+  plan_items(a, x, heads, wcs, nh, [&](int bh, int grp, int lo, int hi) {
+    const int pos = atomicAdd(&start[hi - lo + 1], 1);
+    int e, j;
+    plan_deal(pos, nl, e, j);
+    if (j < kmax) lane_base(e)[j] = ScreenItem{bh, grp, lo, hi};  // j < kmax always (kmax bounds the items)
+  });
+  // positions past each lane's items: empty
+  const int n = total, full = n / nl, r = n - full * nl;
+  for (int e = 0; e < nl; ++e) {
+    const bool extra = r > 0 && ((full & 1) ? e >= nl - r : e < r);
+    ScreenItem* lb = lane_base(e);
+    for (int j = full + (extra ? 1 : 0) + t; j < kmax; j += blockDim.x) lb[j] = ScreenItem{-1, 0, 0, -1};
+  }
+}
+
+// Plan dimensions from the shape alone (the windows live on the device):
+// seg = clamp(ceil(5*nkt/16), 8, 256) key tiles per item, and kmax bounds a
+// lane's items as if every window were unbounded.
+void screen_plan_dims(const Geometry& g, int& seg, int& kmax, int& per_xcd) {
+  seg = (5 * g.nkt + 15) / 16;
+  seg = seg < 8 ? 8 : (seg > 256 ? 256 : seg);
+  const int64_t BH = (int64_t)g.B * g.H;
+  // global mode for few heads; per-XCD mode keeps at most kPlanMaxHeads per XCD
+  per_xcd = BH >= 32 ? 1 : 0;
+  const int ngroups = (g.nqt + 3) / 4;
+  int64_t per_head = 0;
+  for (int grp = 0; grp < ngroups; ++grp) {
+    const int64_t qa = (int64_t)grp * 4 * kTile;
+    const int64_t qb = qa + 4 * kTile - 1 < g.Tq - 1 ? qa + 4 * kTile - 1 : g.Tq - 1;
+    const int64_t jhi = g.causal ? (qb < g.Tk - 1 ? qb : g.Tk - 1) : g.Tk - 1;
+    const int64_t steps = jhi >= 0 ? jhi / kTile + 1 : 0;
+    per_head += (steps + seg - 1) / seg;
+  }
+  const int64_t items = per_xcd ? (BH + 7) / 8 * per_head : BH * per_head;
+  const int64_t k = (items + (per_xcd ? 4 : 32) - 1) / (per_xcd ? 4 : 32);
+  kmax = (int)(k > 0 ? k : 1);
+}
+size_t screen_plan_bytes(const Geometry& g) {
+  int seg, kmax, per_xcd;
+  screen_plan_dims(g, seg, kmax, per_xcd);
+  return round_up((int64_t)32 * kmax * (int64_t)sizeof(ScreenItem), 256);
+}
 
 // 16-byte chunk per thread per row; a key row of DP elements spans CPR
 // threads, and a thread covers kPrepRows rows RPB apart (all loads first).
@@ -42,7 +275,11 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
   constexpr int VEC = 16 / (int)sizeof(T);
   constexpr int CPR = DP / VEC;  // chunks per row (power of two, <= 32)
   constexpr int RPB = 256 / CPR;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  if (blockIdx.y == 0) {  // the first row plans the screen, one block per XCD
+    if (blockIdx.x < 8) screen_plan(a, blockIdx.x);
+    return;
+  }
+  const int bh = blockIdx.y - 1, b = bh / a.H, h = bh % a.H;
   const int d0 = (threadIdx.x % CPR) * VEC;
   float x[kPrepRows][VEC];
 #pragma unroll
@@ -87,9 +324,9 @@ struct FwdKArgs {
   void* y; float* hnorm; uint32_t* bits;
   Dropout drop;
   int H, Tq, Tk, D, nqt, nku_words, causal;
-  int nsegl;  // screen blocks per 4-query-tile group (segment stride)
   int64_t Tk_pad;
   float eps;
+  ScreenPlan plan;
 };
 
 // Range [lo, hi] of the U-key blocks that hold the window of queries [qa, qb].
@@ -115,57 +352,21 @@ struct ScreenTile {
   static constexpr int TILEB = 64 * ROWB;            // bytes per staged key tile
   static constexpr int CPT = 64 * CPR / 256;         // DMA chunks per thread per tile
   static constexpr int NST = 4;                      // pipeline stages (3 tiles in flight)
-  static constexpr int SEG = 256;                    // key tiles per work segment
   // LDS chunk position of global chunk c of row R: c ^ swz(R), conflict-free
   // for the perm_row operand reads
   __device__ static inline int swz(int R) { return lds_swz<CPR>(R); }
 };
-constexpr int kScreenSegBlocks = 8;  // max blocks per query-tile group
-
-// Block order of the screen.  A head's cost grows with its window, and its
-// key tiles are re-read by every query group, so a head stays on one XCD (one
-// L2) and the heads are dealt to the 8 XCDs by window size: ranks (widest
-// first) 0..7 go to XCDs 0..7, ranks 8..15 to XCDs 7..0, and so on, which
-// evens out the XCDs' total work.  Each XCD runs its heads widest first and,
-// within a head, the longest (last) query groups first.  Blocks are
-// dispatched round-robin over the XCDs in linear order, so linear block p
-// runs on XCD p % 8.  Other shapes fall back to xcd_order.
-__device__ inline void screen_order(const FwdKArgs& a, int& bx, int& bh) {
-  const int nx = gridDim.x, BH = gridDim.y;
-  if ((BH & 7) != 0 || BH > 64) {
-    xcd_order(bx, bh);
-    return;
-  }
-  const int p = blockIdx.x + nx * blockIdx.y;
-  const int x = p & 7, s = p >> 3;
-  const int jh = s / nx;                                 // this XCD's jh-th head
-  const int k = 8 * jh + ((jh & 1) ? 7 - x : x);         // its rank, widest first
-  // ranks on the total order (window key, index) of window_rank_key: a
-  // permutation of the B*H heads even with NaN or repeated windows
-  const int lane = threadIdx.x & 63;
-  const float wl = window_rank_key(lane < BH ? a.w[lane % a.H] : 0.0f);  // lane o holds head o's key
-  int rank = 0;
-  for (int o = 0; o < BH; ++o) {
-    const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), o));
-    rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
-  }
-  const unsigned long long sel = __ballot(lane < BH && rank == k);
-  bh = sel != 0ull ? (int)__builtin_ctzll(sel) : k;  // never empty: ranks are a permutation
-  bx = nx - 1 - (s - jh * nx);
-}
 
 // ---------------------------------------------------------------------------
 // Screen: 256-thread block = 4 waves, wave -> one 64-query tile of one head.
-// The key-tile range of the 4 tiles' windows is cut into segments of SEG
-// tiles; block x = (group, first segment) and the block steps through its
-// group's segments with stride nsegl, so the work per block stays bounded
-// whatever the window.  Within a segment the key tiles stream through a
-// 4-stage LDS ring filled by direct global->LDS DMA three tiles ahead (no
-// register staging, one raw barrier per tile).  Chunks are XOR-swizzled
+// Each block runs one item of the plan (prep_k_kernel): a 4-query-tile group
+// of one head and a range [lo, hi] of the key tiles of its window.  The key
+// tiles stream through a 4-stage LDS ring filled by direct global->LDS DMA
+// three tiles ahead (no register staging, one raw barrier per tile).  Chunks are XOR-swizzled
 // within each key row so the A-operand reads spread over the LDS banks.  Each wave forms S^T = K^ Q^T on MFMA for the tiles of its own window
 // and votes with a ballot whether any in-window pair passes the
 // trim-and-square threshold; live bits are ORed into the bitmap (cleared by
-// prep_k_kernel), so segments that share a bitmap word need no ordering.
+// prep_k_kernel), so items that share a bitmap word need no ordering.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void fwd_screen_kernel(FwdKArgs a) {
@@ -178,9 +379,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
   const int half = lane >> 5, l32 = lane & 31;
-  int bx, bh;
-  screen_order(a, bx, bh);
-  const int grp = bx / a.nsegl, seg0 = bx % a.nsegl;
+  // this block's item: lane (XCD p % 8, engine (p >> 3) % 4), position p >> 5
+  const int p = blockIdx.x;
+  const ScreenItem item = a.plan.table[((p & 7) * 4 + ((p >> 3) & 3)) * a.plan.kmax + (p >> 5)];
+  if (item.bh < 0) return;  // block-uniform: past this lane's items
+  const int bh = item.bh, grp = item.grp, slo = item.lo, shi = item.hi;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);
@@ -188,14 +391,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const bool wave_ok = qt < a.nqt;
   const int q0 = qt * kTile;
 
-  int kt_lo, kt_hi, blo, bhi;
+  int kt_lo, kt_hi;
   key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
   if (!wave_ok) { kt_lo = 0; kt_hi = -1; }
-  {
-    const int64_t bq0 = (int64_t)grp * 4 * kTile;
-    key_tile_range(a, hp, causal, bq0, bq0 + 4 * kTile - 1 < a.Tq - 1 ? bq0 + 4 * kTile - 1 : a.Tq - 1, blo, bhi);
-  }
-  if (blo + seg0 * G::SEG > bhi) return;  // block-uniform: no segment for this block
 
   // own query rows (raw B operands); their 1/|q| is formed once the first
   // key tiles' DMA is in flight behind them
@@ -312,15 +510,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   };
 
-  // Tiles past a segment's last tile shi are replaced by shi itself: the ring
+  // Tiles past the item's last tile shi are replaced by shi itself: the ring
   // slot they fill is free and never read, and every step then waits for the
   // same count.
-  auto prologue = [&](int slo, int shi) {
 #pragma unroll
-    for (int n = 0; n < NST - 1; ++n) issue(slo + n <= shi ? slo + n : shi, n);
-  };
-  auto seg_end = [&](int slo) { return slo + G::SEG - 1 < bhi ? slo + G::SEG - 1 : bhi; };
-  prologue(blo + seg0 * G::SEG, seg_end(blo + seg0 * G::SEG));
+  for (int n = 0; n < NST - 1; ++n) issue(slo + n <= shi ? slo + n : shi, n);
 #pragma unroll
   for (int qh = 0; qh < 2; ++qh) {
     iq[qh] = qrow[qh].inv_norm(a.eps);
@@ -328,12 +522,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = qrow[qh].f[ks];
   }
 
-  for (int sg = seg0;; sg += a.nsegl) {
-    const int slo = blo + sg * G::SEG;
-    if (slo > bhi) break;
-    const int shi = seg_end(slo);
-    if (sg != seg0) prologue(slo, shi);
-
+  {
     // Software pipeline over the two 32-key halves of each tile: the vote on
     // one half runs while the MFMAs of the next half are in flight.  Order in
     // step kt: MFMA(kt, keys 0-31) -> finish tile kt-1 (vote on its keys
@@ -399,10 +588,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     for (; kt <= shi; ++kt) step(kt);
     if (pend) finish(shi, live0, vote_half(acc1, pk0, 1, pint));
-    // the replacement loads are done and every wave is done with the ring
-    // before the next segment refills it
+    // the trailing replacement loads land before the block ends
     wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
   }
   guard_frags(qf);
 }
@@ -619,41 +806,46 @@ void fwd_live_kernel(FwdKArgs a) {
   }
 }
 
-size_t fwd_ws_bytes(const Geometry& g) {
+static int64_t khat_bytes(const Geometry& g) {
   return round_up((int64_t)g.B * g.H * g.Tk_pad * g.DP * (int64_t)g.esize, 256);
 }
+// Workspace: [K^][screen plan table]
+size_t fwd_ws_bytes(const Geometry& g) { return khat_bytes(g) + screen_plan_bytes(g); }
 
 template <typename T, int DP>
 static hipError_t launch_fwd_t(const FwdCall& c) {
   const Geometry& g = c.g;
-  if (g.Tk_pad > 0) {
-    PrepKArgs pa;
-    pa.k = c.k; pa.ks = c.ks; pa.kpm = c.kpm; pa.khat = c.khat;
-    pa.bits = c.bits; pa.bits_per_bh = (int64_t)2 * g.nqt * g.nku_words;
-    pa.H = g.H; pa.Tk = g.Tk; pa.D = g.D; pa.Tk_pad = g.Tk_pad; pa.eps = c.eps;
-    constexpr int RPB = 256 / (DP * (int)sizeof(T) / 16) * kPrepRows;
-    timer_begin(1, c.stream);
-    hipLaunchKernelGGL((prep_k_kernel<T, DP>), dim3((unsigned)((g.Tk_pad + RPB - 1) / RPB), (unsigned)(g.B * g.H)),
-                       dim3(256), 0, c.stream, pa);
-    timer_end(1, c.stream);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  ScreenPlan plan;
+  screen_plan_dims(g, plan.seg, plan.kmax, plan.per_xcd);
+  plan.table = (ScreenItem*)((char*)c.khat + khat_bytes(g));
   FwdKArgs fa;
   fa.q = c.q; fa.qs = c.qs; fa.v = c.v; fa.vs = c.vs; fa.khat = c.khat;
   fa.r = c.r; fa.w = c.w; fa.y = c.y; fa.hnorm = c.hnorm; fa.bits = c.bits;
   fa.H = g.H; fa.Tq = g.Tq; fa.Tk = g.Tk; fa.D = g.D; fa.nqt = g.nqt; fa.nku_words = g.nku_words;
   fa.causal = g.causal; fa.Tk_pad = g.Tk_pad; fa.eps = c.eps; fa.drop = c.drop;
-  {
-    const int nseg = (g.nkt + ScreenTile<T, DP>::SEG - 1) / ScreenTile<T, DP>::SEG;
-    fa.nsegl = nseg < kScreenSegBlocks ? (nseg > 0 ? nseg : 1) : kScreenSegBlocks;
+  fa.plan = plan;
+  if (g.Tk_pad > 0) {  // no keys: no bitmap words and no screen work
+    PrepKArgs pa;
+    pa.k = c.k; pa.ks = c.ks; pa.kpm = c.kpm; pa.khat = c.khat;
+    pa.bits = c.bits; pa.bits_per_bh = (int64_t)2 * g.nqt * g.nku_words;
+    pa.B = g.B; pa.H = g.H; pa.Tq = g.Tq; pa.Tk = g.Tk; pa.D = g.D; pa.nqt = g.nqt; pa.causal = g.causal;
+    pa.Tk_pad = g.Tk_pad; pa.eps = c.eps;
+    pa.r = c.r; pa.w = c.w; pa.plan = plan;
+    constexpr int RPB = 256 / (DP * (int)sizeof(T) / 16) * kPrepRows;
+    const int64_t nx = (g.Tk_pad + RPB - 1) / RPB;
+    // row 0: the screen planner (8 blocks); rows 1..B*H: K^ of head row-1
+    timer_begin(1, c.stream);
+    hipLaunchKernelGGL((prep_k_kernel<T, DP>), dim3((unsigned)(nx > 8 ? nx : 8), (unsigned)(g.B * g.H + 1)),
+                       dim3(256), 0, c.stream, pa);
+    timer_end(1, c.stream);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    timer_begin(2, c.stream);
+    hipLaunchKernelGGL((fwd_screen_kernel<T, DP>), dim3((unsigned)(32 * plan.kmax)), dim3(256), 0, c.stream, fa);
+    timer_end(2, c.stream);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
-  timer_begin(2, c.stream);
-  hipLaunchKernelGGL((fwd_screen_kernel<T, DP>), dim3((unsigned)((g.nqt + 3) / 4 * fa.nsegl), (unsigned)(g.B * g.H)),
-                     dim3(256), 0, c.stream, fa);
-  timer_end(2, c.stream);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   timer_begin(3, c.stream);
   hipLaunchKernelGGL((fwd_live_kernel<T, DP>), dim3((unsigned)(2 * g.nqt), (unsigned)(g.B * g.H)), dim3(64), 0,
                      c.stream, fa);
