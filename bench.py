@@ -13,7 +13,12 @@ Also reported:
   cpu_baseline  the reference's dense torch-fp32 math on the host cores, on a
                 bounded sample, scaled to the same unit
   decode        the T=100K single-query decode kernel (configs[4] shape) in
-                GB/s against HBM peak
+                GB/s against HBM peak (decode-stream variant: every key in window)
+  cfg3_lm_train_step   configs[2]: one MultiscreenLM training step, tokens/s
+                       and the attention kernels' share of it
+  cfg4_prefill_100k    configs[3]: the T=100,000 prefill forward, with its
+                       algorithmic flop C(|W|+|A|) and bf16-peak fraction
+  cfg5_decode_literal  configs[4] as written: ms per generated token
 Prints ONE JSON line.
 """
 
@@ -41,6 +46,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--no-configs", action="store_true", help="skip the configs[2..4] legs")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--calib-copy", action="store_true",
                    help="end with one elementwise pass over 2 GiB (rocprofv3 --pmc byte-counter calibration)")
@@ -190,6 +196,140 @@ def decode_bench(L, ops, torch, steps=20):
             "live_v_rows": live, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
+VOCAB = 50257
+
+
+def zipf_ids(B, T, s, seed):
+    """Token ids drawn from a Zipf(s) distribution over the vocabulary, p(k) ~ (k+1)^-s."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    p = torch.arange(1, VOCAB + 1, dtype=torch.float64).pow(-s)
+    return torch.multinomial((p / p.sum()).float(), B * T, replacement=True, generator=g).view(B, T)
+
+
+def _kernel_sum_ms(L, fn, ids=(1, 2, 3, 4, 5), per_call=200):
+    """Sum of the durations (ms) of the library's kernels launched by one call of fn."""
+    import ctypes
+    for kid in ids:
+        assert L.msa_timer_arm(kid, per_call) == 0
+    fn()
+    total = 0.0
+    buf = (ctypes.c_float * per_call)()
+    for kid in ids:
+        n = L.msa_timer_read(kid, buf, per_call)
+        total += sum(buf[i] for i in range(max(n, 0)))
+    L.msa_timer_arm(0, 0)
+    return total
+
+
+def cfg3_bench(L, torch, steps=5, warmup=2):
+    """one training step of MultiscreenLM(50257, 512, 8 heads, 6 layers,
+    max_seq_len 2048), random init (seed 0), fp32 master weights under bf16 autocast, on 8 x 2048
+    Zipf(1.1) ids with labels = ids: forward + loss, backward, clip_grad_norm_(1.0) and AdamW step
+    (train.py:96-104).  Attention share: the library's kernels (6 layers, fwd + bwd) over the step."""
+    from multiscreen import MultiscreenLM
+    torch.manual_seed(0)
+    lm = MultiscreenLM(vocab_size=VOCAB, d_model=512, num_heads=8, num_layers=6, max_seq_len=2048).cuda()
+    opt = torch.optim.AdamW(lm.parameters(), lr=3e-4, weight_decay=0.1)
+    ids = zipf_ids(8, 2048, 1.1, seed=0).cuda()
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = lm(ids, labels=ids)["loss"]
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(lm.parameters(), 1.0)
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        loss = step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    attn_ms = _kernel_sum_ms(L, step)
+    torch.cuda.synchronize()
+    return {"workload": "configs[2]: MultiscreenLM(50257,512,8,6,2048) training step, 8x2048 Zipf(1.1) ids, "
+                        "bf16 autocast, AdamW + clip",
+            "ms_per_step": round(ms, 3), "tokens_per_s": round(8 * 2048 / (ms * 1e-3), 1),
+            "attention_kernels_ms": round(attn_ms, 3), "attention_share": round(attn_ms / ms, 4),
+            "loss": round(float(loss.detach()), 4)}
+
+
+def cfg4_bench(L, ops, torch, reps=5):
+    """long-context prefill forward, B=1, T=100,000, H=8, D=64, bf16,
+    causal, r=2, w log-uniform in [512, 1e5] (seed 4); q, k, v ~ N(0,1) drawn on the CPU."""
+    B, T, H, D = 1, 100000, 8, 64
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(B, T, H, D, generator=g).bfloat16().cuda() for _ in range(3))
+    lo, hi = math.log(512.0), math.log(1e5)
+    w = torch.exp(lo + (hi - lo) * torch.rand(H, generator=g)).tolist()
+    rg, wg = torch.full((H,), 2.0, device="cuda"), torch.tensor(w, device="cuda")
+    fn = lambda: ops.fwd_raw(q, k, v, rg, wg, True, 1e-8, None)
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        y, hn, bits = fn()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    screen_ms, _ = kernel_times(L, 2, fn, 3)
+    nW = window_tiles(T, w) * B
+    nU, nA = live_counts(bits, B, H, T)
+    flop = TILE_FLOP * (nW + nA)
+    causal_tiles = B * H * ((T + 63) // 64) * ((T + 63) // 64 + 1) // 2
+    return {"workload": "configs[3]: prefill forward B=1 T=100000 H=8 D=64 bf16 causal, r=2, w log-U[512,1e5]",
+            "w": [round(x, 1) for x in w], "ms": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "tiles": {"causal": causal_tiles, "window": nW, "active": nA, "active_units_32": nU},
+            "flop_alg": flop, "tflops_alg": round(flop / (ms * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 5),
+            "screen_kernel_ms": round(screen_ms, 4),
+            "screen_frac_bf16_peak": round(TILE_FLOP * nW / (screen_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 5)}
+
+
+def cfg5_bench(torch, new_tokens=256):
+    """BASELINE.json configs[4] as written: MultiscreenLM(50257, 512, 8 heads, 6 layers,
+    max_seq_len 100000) at random init (seed 0, so the init windows 2..256 and r = 2), bf16
+    weights and bf16 KV caches of 100,000 positions, batch 16, prompts of 100000-256 uniform
+    ids (seed 0), prefill then 256 greedy tokens (MultiscreenLM.generate, top_k=1)."""
+    from multiscreen import MultiscreenLM
+    B, CAP = 16, 100000
+    torch.manual_seed(0)
+    lm = MultiscreenLM(vocab_size=VOCAB, d_model=512, num_heads=8, num_layers=6,
+                       max_seq_len=CAP).to("cuda", torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, VOCAB, (B, CAP - new_tokens), generator=g).cuda()
+    caches = lm.new_cache(B, CAP, torch.bfloat16, "cuda")
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = lm.prefill(prompt, caches)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        tok = logits.argmax(-1, keepdim=True)
+        for s in range(4):  # untimed warm-up of the decode path (positions overwritten below)
+            lm.decode_step(tok, caches, CAP - new_tokens + s)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(new_tokens - 1):
+            logits = lm.decode_step(tok, caches, CAP - new_tokens + s)
+            tok = logits.argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t_dec = time.perf_counter() - t0
+    return {"workload": "configs[4]: MultiscreenLM 6 layers, B=16, bf16 KV cache 100000, init windows, "
+                        "prefill + 256 greedy tokens",
+            "prefill_s": round(t_prefill, 4), "ms_per_token": round(t_dec / (new_tokens - 1) * 1e3, 4),
+            "tokens_per_s": round(B * (new_tokens - 1) / t_dec, 1)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -288,11 +428,23 @@ def main():
                   "threshold_skip": round(1 - nA / nW, 5)},
         "step_tflops_alg": round(step_tflops, 2),
         "step_frac_bf16_peak": round(step_tflops / PEAK_BF16_TFLOPS, 5),
-        "kernel_ms": {k_: round(v_, 4) for k_, v_ in breakdown.items()},
+        "kernel_ms_event": {k_: round(v_, 4) for k_, v_ in breakdown.items()},
+        "kernel_ms_note": "HIP events around each launch, outside the timed region: each includes its "
+                          "launch gap (about 1-3 us), so they sum past ms_per_step; profiles/ has the "
+                          "rocprofv3 durations",
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_decode:
         out["decode"] = decode_bench(L, ops, torch)
+    if not args.no_configs:
+        for key, leg in (("cfg3_lm_train_step", lambda: cfg3_bench(L, torch)),
+                         ("cfg4_prefill_100k", lambda: cfg4_bench(L, ops, torch)),
+                         ("cfg5_decode_literal", lambda: cfg5_bench(torch))):
+            try:
+                out[key] = leg()
+            except Exception as e:  # reported in the line, not hidden
+                out[key] = {"error": f"{type(e).__name__}: {e}"}
+            torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, H, D, r, w, args.seed)
     if args.calib_copy:

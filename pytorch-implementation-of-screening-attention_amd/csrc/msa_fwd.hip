@@ -45,6 +45,7 @@ namespace msa {
 // Which items run where changes only the time, never the bitmap (live bits
 // are ORed).
 // ---------------------------------------------------------------------------
+constexpr int kScreenBlocksPerLane = 256;
 struct ScreenItem {
   int bh, grp, lo, hi;  // head, 4-query-tile group, key tiles [lo, hi]
 };
@@ -379,10 +380,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
   const int half = lane >> 5, l32 = lane & 31;
-  // this block's item: lane (XCD p % 8, engine (p >> 3) % 4), position p >> 5
+  // this block's lane: (XCD p % 8, engine (p >> 3) % 4); it runs the lane's
+  // items at positions p >> 5, (p >> 5) + K, ... (K blocks per lane), which
+  // are sorted longest first and end with empty entries
   const int p = blockIdx.x;
-  const ScreenItem item = a.plan.table[((p & 7) * 4 + ((p >> 3) & 3)) * a.plan.kmax + (p >> 5)];
-  if (item.bh < 0) return;  // block-uniform: past this lane's items
+  const ScreenItem* lane_items = a.plan.table + ((p & 7) * 4 + ((p >> 3) & 3)) * a.plan.kmax;
+  const int kstride = (int)(gridDim.x >> 5);
+  for (int pos = p >> 5; pos < a.plan.kmax; pos += kstride) {
+  const ScreenItem item = lane_items[pos];
+  if (item.bh < 0) break;  // block-uniform: past this lane's items
   const int bh = item.bh, grp = item.grp, slo = item.lo, shi = item.hi;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
@@ -417,8 +423,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
   for (int u = 0; u < G::CPT; ++u) {
     const int c = u * 256 + tid;
-    const int row = c / G::CPR, p = c % G::CPR;
-    goff[u] = (uint32_t)(row * G::ROWB + ((p ^ G::swz(row)) << 4));
+    const int row = c / G::CPR, pc = c % G::CPR;
+    goff[u] = (uint32_t)(row * G::ROWB + ((pc ^ G::swz(row)) << 4));
   }
   // ring slot of the n-th tile of a segment: n % NST
   auto issue = [&](int kt, int slot_idx) {
@@ -588,10 +594,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     for (; kt <= shi; ++kt) step(kt);
     if (pend) finish(shi, live0, vote_half(acc1, pk0, 1, pint));
-    // the trailing replacement loads land before the block ends
+    // the trailing replacement loads have landed and every wave is done with
+    // the ring before the next item refills it
     wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
   }
   guard_frags(qf);
+  }  // item loop
 }
 
 // ---------------------------------------------------------------------------
@@ -841,7 +850,10 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     timer_begin(2, c.stream);
-    hipLaunchKernelGGL((fwd_screen_kernel<T, DP>), dim3((unsigned)(32 * plan.kmax)), dim3(256), 0, c.stream, fa);
+    // at most kScreenBlocksPerLane blocks per lane; blocks beyond the first
+    // walk their lane's items with that stride
+    const int per_lane = plan.kmax < kScreenBlocksPerLane ? plan.kmax : kScreenBlocksPerLane;
+    hipLaunchKernelGGL((fwd_screen_kernel<T, DP>), dim3((unsigned)(32 * per_lane)), dim3(256), 0, c.stream, fa);
     timer_end(2, c.stream);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
