@@ -23,6 +23,7 @@ import math
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from .norm import TanhNorm
 from . import ops
@@ -73,6 +74,45 @@ class ScreeningAttention(nn.Module):
         """proj(x) viewed as (B, T, H, D) -- no copy (attention.py:150-151)."""
         return proj(x).view(x.shape[0], x.shape[1], self.num_heads, self.head_dim)
 
+    def _fused_weight(self, projs) -> torch.Tensor:
+        """The projections' weights stacked along the output dimension.  Under
+        autograd the concatenation is part of the graph (its backward splits
+        the gradient back to each Linear); without it the stacked weight is
+        kept and rebuilt only when a weight changes (in-place updates bump
+        their version counters)."""
+        ws = [p.weight for p in projs]
+        if torch.is_grad_enabled():
+            return torch.cat(ws)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        cache = self.__dict__.get("_fused_cache", {})
+        hit = cache.get(len(ws))
+        if hit is None or hit[0] != key:
+            hit = (key, torch.cat(ws))
+            cache[len(ws)] = hit
+            self.__dict__["_fused_cache"] = cache
+        return hit[1]
+
+    def project_qkv(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor):
+        """q, k, v projections as (B, T, H, D) views (attention.py:147-153) from
+        as few GEMMs as the inputs allow: one over the stacked q/k/v weights
+        for self-attention (query is key is value), one for q and one over the
+        stacked k/v weights when key is value (cross-attention over a memory),
+        else three.  The views' time stride is then 3*d_model (or 2*d_model);
+        the fused kernels read them in place."""
+        B, Tq, _ = query.shape
+        Tk = key.shape[1]
+        H, D, d = self.num_heads, self.head_dim, self.d_model
+        if query is key and key is value:
+            qkv = F.linear(query, self._fused_weight((self.q_proj, self.k_proj, self.v_proj)))
+            q, k, v = qkv.split(d, dim=-1)
+            return q.view(B, Tq, H, D), k.view(B, Tq, H, D), v.view(B, Tq, H, D)
+        q = self.project(query, self.q_proj)
+        if key is value:
+            kv = F.linear(key, self._fused_weight((self.k_proj, self.v_proj)))
+            k, v = kv.split(d, dim=-1)
+            return q, k.view(B, Tk, H, D), v.view(B, Tk, H, D)
+        return q, self.project(key, self.k_proj), self.project(value, self.v_proj)
+
     def core(self, q, k, v, key_padding_mask=None):
         """(B,T,H,D) raw projections -> TanhNorm'd (B,Tq,H,D) head outputs."""
         w, r = self.window(), self.sharpness()
@@ -100,9 +140,7 @@ class ScreeningAttention(nn.Module):
             out: (B, T_q, d_model)
         """
         B, T_q, _ = query.shape
-        q = self.project(query, self.q_proj)
-        k = self.project(key, self.k_proj)
-        v = self.project(value, self.v_proj)
+        q, k, v = self.project_qkv(query, key, value)
         y = self.core(q, k, v, key_padding_mask)
         return self.out_proj(y.reshape(B, T_q, self.d_model))
 
@@ -117,7 +155,7 @@ class ScreeningAttention(nn.Module):
         """Causal self-attention forward over x (B,T,d) at positions 0..T-1;
         also writes its k/v projections into cache[:, :T]."""
         B, T, _ = x.shape
-        q, k, v = self.project(x, self.q_proj), self.project(x, self.k_proj), self.project(x, self.v_proj)
+        q, k, v = self.project_qkv(x, x, x)
         cache.store(k, v, 0)
         y = self.core(q, k, v)
         return self.out_proj(y.reshape(B, T, self.d_model))
@@ -127,7 +165,7 @@ class ScreeningAttention(nn.Module):
         if not self.causal:
             raise RuntimeError("KV-cache decode is defined for causal self-attention only")
         B = x.shape[0]
-        q, k, v = self.project(x, self.q_proj), self.project(x, self.k_proj), self.project(x, self.v_proj)
+        q, k, v = self.project_qkv(x, x, x)
         cache.store(k, v, pos)
         kc, vc = cache.k[:, :pos + 1], cache.v[:, :pos + 1]
         w, r = self.window(), self.sharpness()

@@ -178,3 +178,37 @@ def test_module_cpu_matches_reference_golden(name):
     assert rel_err(np64(x.grad), z["dx"]) < 1e-5
     assert rel_err(np64(m.s_r.grad), z["ds_r"]) < 1e-5
     assert rel_err(np64(m.s_v.grad), z["ds_v"]) < 1e-5
+
+
+def test_fused_qkv_projection_matches_separate_linears():
+    # one GEMM over the stacked q/k/v weights (self-attention) or k/v weights
+    # (cross-attention) gives the three projections; state_dict keys unchanged
+    from multiscreen import ScreeningAttention
+    torch.manual_seed(0)
+    m = ScreeningAttention(64, 4)
+    x, mem = torch.randn(2, 9, 64), torch.randn(2, 5, 64)
+    sep = [m.project(t, p) for t, p in ((x, m.q_proj), (x, m.k_proj), (x, m.v_proj))]
+    for got, want in zip(m.project_qkv(x, x, x), sep):
+        assert got.shape == (2, 9, 4, 16)
+        torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-6)
+    got = m.project_qkv(x, mem, mem)
+    for t, p, g in ((x, m.q_proj, got[0]), (mem, m.k_proj, got[1]), (mem, m.v_proj, got[2])):
+        torch.testing.assert_close(g, m.project(t, p), rtol=1e-6, atol=1e-6)
+    assert sorted(k for k in m.state_dict() if k.endswith("weight")) == \
+        ["k_proj.weight", "out_proj.weight", "q_proj.weight", "v_proj.weight"]
+    # gradients reach each Linear through the stacked weight
+    m.project_qkv(x, x, x)[1].sum().backward()
+    assert m.k_proj.weight.grad.abs().sum() > 0
+    assert m.q_proj.weight.grad is None or m.q_proj.weight.grad.abs().sum() == 0
+
+
+def test_fused_weight_cache_follows_in_place_updates():
+    from multiscreen import ScreeningAttention
+    torch.manual_seed(1)
+    m = ScreeningAttention(32, 2)
+    x = torch.randn(1, 4, 32)
+    with torch.no_grad():
+        a = m.project_qkv(x, x, x)[2].clone()
+        m.v_proj.weight.mul_(2.0)           # in place: bumps the version counter
+        b = m.project_qkv(x, x, x)[2]
+    torch.testing.assert_close(b, 2.0 * a, rtol=1e-6, atol=1e-6)
