@@ -27,15 +27,17 @@ constexpr int kUnit = 32;  // rows of a query unit and of a key unit (live-unit 
 // whatever that mapping is.
 //   C/D layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
 //
-// Source-operand guard.  With this toolchain (ROCm 7.2 clang, gfx950) a VALU
-// instruction may be scheduled to overwrite the A/B source VGPRs of a
-// v_mfma_f32_32x32x16_bf16 within a few cycles of its issue, with no wait
-// states in between, and the MFMA then reads the new values: measured on an
-// MI355X, 2 and 4 wait states still corrupted the product, 8 did not.  After
-// every MFMA an s_nop block that takes A and B as read-write operands keeps
-// those registers from being reused until 16 wait states have passed.  The
-// MFMA pipe is busy far longer than that per instruction, so back-to-back
-// MFMA throughput is unchanged.
+// Source-operand guard.  This toolchain (ROCm 7.2 clang, gfx950) schedules a
+// VALU or LDS write into the A/B source VGPRs of an MFMA as if the MFMA had
+// read them at issue.  An MFMA whose accumulator comes from the MFMA before it
+// waits for that result and reads A/B later, so it can read the new values.
+// The unguarded D=32 bf16 dq kernel shows a v_mov_b64 refilling SrcA one
+// instruction after such a chained v_mfma_f32_32x32x16_bf16.  Measured on an
+// MI355X: 2 and 4 wait states of padding still corrupted the product, 8 did
+// not.  After every MFMA group an s_nop block that takes A and B as read-write
+// operands keeps those registers from being reused until 16 wait states have
+// passed.  The MFMA pipe is busy far longer than that per instruction, so
+// back-to-back MFMA throughput is unchanged.
 // ---------------------------------------------------------------------------
 template <typename T> struct Mma;
 
@@ -236,9 +238,11 @@ __device__ inline uint32_t pass_mask(const f32x16& c, float th) {
 // Indexed form: a loop over the set bits only, r uniform, so c[r] inside fn
 // is a register-indexed move (s_set_gpr_idx), not a memory access.  Unrolled
 // form: a compile-time r and one uniform branch per register.  The fp32
-// kernels, whose register files are full (accumulators partly in AGPRs), use
-// the unrolled form: with the indexed one their dK parity test failed, and
-// the cause is not established.
+// kernels use the unrolled form.  Their S/dP accumulation is a dependent chain
+// of 16-pass v_mfma_f32_32x32x2_f32 reading B from the registers that the
+// indexed loop's copies of s and dP reuse.  Those writes come 27-32 wait
+// states after the chain's last issue, which the 16-wait-state guard does not
+// cover.  With the indexed form the fp32 dK parity test failed.
 template <bool kIndexed, typename Fn>
 __device__ inline void for_each_set(uint32_t pm, Fn&& fn) {
   if constexpr (kIndexed) {
