@@ -474,17 +474,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // is monotone in s and s = acc/|q_i|, so a 32x32 unit has a live pair iff
   // its largest in-window acc passes.  Register r of the half holds key
   // k0 + 32kh + 16(r/8) + 8half + r%8.  Tiles wholly inside every pair's
-  // window skip the per-register window test.  Bit qh of the result: this
-  // lane's query of unit qh passes.
+  // window skip the per-register window test; in the other tiles each 32x32
+  // unit is classed by its distance range c-31 .. c+31 (the window is one
+  // interval of distances): wholly inside (plain maximum), wholly outside (no
+  // vote) or cut by a window edge (per-register test).  Bit qh of the result:
+  // this lane's query of unit qh passes.
   auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh, bool interior) -> int {
     int lv = 0;
 #pragma unroll
     for (int qh = 0; qh < 2; ++qh) {
       float mx = -INFINITY;
-      if (interior) {
+      const int c = q0 + 32 * qh - k0 - 32 * kh;  // wave-uniform
+      if (interior || (in_window(c - 31, hp) && in_window(c + 31, hp))) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[qh][r]);
-      } else {
+      } else if (c + 31 + hp.wsh >= 0 && c - 31 + hp.wsh < (int)hp.wlim) {
         const int rel0 = (q0 + 32 * qh + l32) - k0 - 32 * kh - 8 * half;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
