@@ -5,19 +5,20 @@
 //                   is folded in as a zero row (s = 0 gives alpha = 0: r > 1).
 //                   Its first row of blocks plans the screen's work (below).
 //   fwd_screen_kernel : 256-thread block = 4 waves, wave -> one 64-query tile
-//                   of one head.  Key tiles of the block's window are copied
-//                   global -> LDS by direct DMA into a 4-slot ring (3 tiles in
-//                   flight) and shared by the 4 waves.  Each wave forms
+//                   of one head; in step n every wave takes the key tile at
+//                   the same tile offset from its query tile, so the waves
+//                   reach the window's edges together.  Key tiles stream
+//                   global -> LDS by direct DMA into a ring (each tile is read
+//                   by the 4 waves in 4 consecutive steps).  Each wave forms
 //                   S^T = K^ Q^T on MFMA (raw bf16 Q, fp32 accumulation, scaled
-//                   by 1/|q_i|) and votes, with a wave ballot, whether any
-//                   in-window pair passes the trim-and-square threshold
-//                   (attention.py:75-90).  Output: the live-tile bitmap.
-//   fwd_live_kernel : 256-thread block per 64-query tile, one 32x32 quadrant
-//                   per wave; walks the tile's live bits, recomputes S^T for
-//                   those key tiles only, forms alpha*m (attention.py:92-119)
-//                   and accumulates H^T += V^T P^T with 1/|v_j| folded into P.
-//                   The epilogue applies TanhNorm (norm.py:23-25) and writes y
-//                   in (B,T,H,D) and |h| per row.
+//                   by 1/|q_i|) and votes whether any in-window pair passes the
+//                   trim-and-square threshold (attention.py:75-90).  Output:
+//                   the live-unit bitmap (32x32 units).
+//   fwd_live_kernel : one wave per 32-query unit; walks the unit's live bits,
+//                   recomputes S^T for those key units only, forms alpha*m
+//                   (attention.py:92-119) and accumulates H^T += V^T P^T with
+//                   1/|v_j| folded into P.  The epilogue applies TanhNorm
+//                   (norm.py:23-25) and writes y in (B,T,H,D) and |h| per row.
 //                   No T x T matrix is ever materialised.
 #include "msa_device.h"
 #include "msa_internal.h"
@@ -31,8 +32,9 @@ namespace msa {
 // per-block hardware-id stamps); only the choice among the engine's 8 CUs is
 // dynamic.  So a launch is 32 "lanes" (XCD, engine) of 8 CUs, each taking
 // its blocks in order, and the screen's makespan is set by the busiest lane
-// and by its longest block.  The plan cuts each 4-query-tile group's
-// key-tile range into items of at most `seg` tiles, near-equal in length,
+// and by its longest block.  The plan cuts each 4-query-tile group's range
+// of tile offsets (one screen step each) into items of at most `seg` steps,
+// near-equal in length,
 // sorts items longest first and deals them over lanes in boustrophedon
 // order, so every lane gets an equal share and runs its longest items first:
 //   per-XCD mode (B*H >= 32): heads are dealt to XCDs widest window first in
@@ -47,12 +49,12 @@ namespace msa {
 // ---------------------------------------------------------------------------
 constexpr int kScreenBlocksPerLane = 256;
 struct ScreenItem {
-  int bh, grp, lo, hi;  // head, 4-query-tile group, key tiles [lo, hi]
+  int bh, grp, lo, hi;  // head, 4-query-tile group, tile offsets qt - kt in [lo, hi]
 };
 struct ScreenPlan {
   ScreenItem* table;  // [8 XCDs][4 engine lanes][kmax]
   int kmax;           // positions per lane
-  int seg;            // key tiles per item at most (<= 256)
+  int seg;            // steps (tile offsets) per item at most (<= 256)
   int per_xcd;        // 1: per-XCD mode, 0: global mode
 };
 
@@ -68,17 +70,6 @@ struct PrepKArgs {
   const float* r; const float* w;
   ScreenPlan plan;
 };
-
-// Key tiles [lo, hi] holding the window of queries [qa, qb] (empty: hi < lo).
-__device__ inline void window_tiles(int Tk, const HeadParams& hp, bool causal, int64_t qa, int64_t qb, int& lo,
-                                    int& hi) {
-  int64_t jlo = qa - hp.wc + 1;
-  int64_t jhi = causal ? qb : qb + hp.wc - 1;
-  if (jlo < 0) jlo = 0;
-  if (jhi > Tk - 1) jhi = Tk - 1;
-  lo = (int)(jlo / kTile);
-  hi = jhi >= jlo ? (int)(jhi / kTile) : lo - 1;
-}
 
 // Per-XCD mode: the heads of XCD x.  Heads are ranked widest window first
 // (NaN keyed as widest, ties by index: a permutation); rank k goes to XCD
@@ -118,8 +109,33 @@ __device__ inline int plan_wc(float w) {
   return !(c > 0.0f) ? 0 : (c > 1073741824.0f ? 1073741824 : (int)c);
 }
 
-// Visits the planned items: fn(bh, grp, lo, hi) for each (head slot, group)
-// pair's near-equal cut of its key-tile range into ceil(steps / seg) items.
+// Tile offsets o = qt - kt of the key tiles kt in the windows of a group's
+// query tiles qt = 4grp .. 4grp+3 (< nqt): the union of each tile's range
+// [qt - hi, qt - lo] (its key tiles [lo, hi]); false if no tile has a key.
+// Every tile's range is an interval and the intervals overlap, so the union
+// is one interval.  wc <= 2^30 and positions < 2^22: no overflow.
+__host__ __device__ inline bool group_offsets(int Tq, int Tk, int nqt, int wc, bool causal, int grp, int& olo,
+                                              int& ohi) {
+  olo = 0x7fffffff;
+  ohi = -0x7fffffff;
+  for (int w = 0; w < 4; ++w) {
+    const int qt = grp * 4 + w;
+    if (qt >= nqt) break;
+    const int qa = qt * kTile, qb = qa + kTile - 1 < Tq - 1 ? qa + kTile - 1 : Tq - 1;
+    int jlo = qa - wc + 1;
+    int jhi = causal ? qb : (wc - 1 > Tk ? Tk : qb + wc - 1);
+    if (jlo < 0) jlo = 0;
+    if (jhi > Tk - 1) jhi = Tk - 1;
+    if (jhi < jlo) continue;
+    const int a = qt - jhi / kTile, b = qt - jlo / kTile;
+    olo = a < olo ? a : olo;
+    ohi = b > ohi ? b : ohi;
+  }
+  return olo <= ohi;
+}
+
+// Visits the planned items: fn(bh, grp, olo, ohi) for each (head slot, group)
+// pair's near-equal cut of its offset range into ceil(steps / seg) items.
 // heads[slot] and the integer windows wcs[slot] are in LDS for the first
 // kPlanMaxHeads slots; beyond them (per-XCD mode without ranking only) slot
 // jh is head 8*jh + x.
@@ -133,20 +149,15 @@ __device__ inline void plan_items(const PrepKArgs& a, int x, const int* heads, c
     const bool cached = slot < kPlanMaxHeads;
     const int bh = cached ? heads[slot] : 8 * slot + x;
     const int wc = cached ? wcs[slot] : plan_wc(a.w[bh % a.H]);
-    {
-      const int qa = grp * 4 * kTile, qb = qa + 4 * kTile - 1 < a.Tq - 1 ? qa + 4 * kTile - 1 : a.Tq - 1;
-      int jlo = qa - wc + 1;                  // wc <= 2^30 and positions < 2^22: no overflow
-      int jhi = causal ? qb : (wc - 1 > a.Tk ? a.Tk : qb + wc - 1);
-      if (jlo < 0) jlo = 0;
-      if (jhi > a.Tk - 1) jhi = a.Tk - 1;
-      if (jhi < jlo) continue;
-      const int lo = jlo / kTile, steps = jhi / kTile - lo + 1;
-      const int n = (steps + seg - 1) / seg, base = steps / n, rem = steps - base * n;
-      for (int i = 0, s0 = lo; i < n; ++i) {
-        const int len = base + (i < rem ? 1 : 0);
-        fn(bh, grp, s0, s0 + len - 1);
-        s0 += len;
-      }
+    int olo, ohi;
+    if (!group_offsets(a.Tq, a.Tk, a.nqt, wc, causal, grp, olo, ohi)) continue;
+    const int steps = ohi - olo + 1;
+    const int n = (steps + seg - 1) / seg, base = steps / n, rem = steps - base * n;
+    // pieces in the order the screen walks offsets (descending)
+    for (int i = 0, s1 = ohi; i < n; ++i) {
+      const int len = base + (i < rem ? 1 : 0);
+      fn(bh, grp, s1 - len + 1, s1);
+      s1 -= len;
     }
   }
 }
@@ -241,7 +252,7 @@ __device__ void screen_plan(const PrepKArgs& a, int x) {
 }
 
 // Plan dimensions from the shape alone (the windows live on the device):
-// seg = clamp(ceil(5*nkt/16), 8, 256) key tiles per item, and kmax bounds a
+// seg = clamp(ceil(5*nkt/16), 8, 256) steps per item, and kmax bounds a
 // lane's items as if every window were unbounded.
 void screen_plan_dims(const Geometry& g, int& seg, int& kmax, int& per_xcd) {
   seg = (5 * g.nkt + 15) / 16;
@@ -252,11 +263,9 @@ void screen_plan_dims(const Geometry& g, int& seg, int& kmax, int& per_xcd) {
   const int ngroups = (g.nqt + 3) / 4;
   int64_t per_head = 0;
   for (int grp = 0; grp < ngroups; ++grp) {
-    const int64_t qa = (int64_t)grp * 4 * kTile;
-    const int64_t qb = qa + 4 * kTile - 1 < g.Tq - 1 ? qa + 4 * kTile - 1 : g.Tq - 1;
-    const int64_t jhi = g.causal ? (qb < g.Tk - 1 ? qb : g.Tk - 1) : g.Tk - 1;
-    const int64_t steps = jhi >= 0 ? jhi / kTile + 1 : 0;
-    per_head += (steps + seg - 1) / seg;
+    int olo, ohi;
+    if (group_offsets(g.Tq, g.Tk, g.nqt, 1 << 30, g.causal != 0, grp, olo, ohi))
+      per_head += (ohi - olo + 1 + seg - 1) / seg;
   }
   const int64_t items = per_xcd ? (BH + 7) / 8 * per_head : BH * per_head;
   const int64_t k = (items + (per_xcd ? 4 : 32) - 1) / (per_xcd ? 4 : 32);
@@ -352,34 +361,46 @@ struct ScreenTile {
   static constexpr int CPR = ROWB / 16;              // 16-byte chunks per row (power of two)
   static constexpr int TILEB = 64 * ROWB;            // bytes per staged key tile
   static constexpr int CPT = 64 * CPR / 256;         // DMA chunks per thread per tile
-  static constexpr int NST = 4;                      // pipeline stages (3 tiles in flight)
+  // ring slots: the 4 tiles the waves read in a step plus the tiles in flight
+  // (2 for tiles up to 8 KiB: 48 KiB a block, three blocks a CU; 1 above)
+  static constexpr int NS = TILEB <= 8192 ? 6 : 5;
   // LDS chunk position of global chunk c of row R: c ^ swz(R), conflict-free
   // for the perm_row operand reads
   __device__ static inline int swz(int R) { return lds_swz<CPR>(R); }
 };
 
+// Floor and ceiling of x / kTile for any sign.
+__device__ inline int floor_tiles(int x) { return x >= 0 ? x / kTile : -((-x + kTile - 1) / kTile); }
+__device__ inline int ceil_tiles(int x) { return -floor_tiles(-x); }
+
 // ---------------------------------------------------------------------------
-// Screen: 256-thread block = 4 waves, wave -> one 64-query tile of one head.
-// Each block runs one item of the plan (prep_k_kernel): a 4-query-tile group
-// of one head and a range [lo, hi] of the key tiles of its window.  The key
-// tiles stream through a 4-stage LDS ring filled by direct global->LDS DMA
-// three tiles ahead (no register staging, one raw barrier per tile).  Chunks are XOR-swizzled
-// within each key row so the A-operand reads spread over the LDS banks.  Each wave forms S^T = K^ Q^T on MFMA for the tiles of its own window
-// and votes with a ballot whether any in-window pair passes the
-// trim-and-square threshold; live bits are ORed into the bitmap (cleared by
-// prep_k_kernel), so items that share a bitmap word need no ordering.
+// Screen: 256-thread block = 4 waves, wave w -> query tile qt = 4grp + w of
+// one head.  Each block runs one item of the plan (prep_k_kernel): a group
+// and a range [olo, ohi] of tile offsets o = qt - kt.  Step n takes offset
+// o = ohi - n for all four waves at once, so wave w reads key tile
+// kt = 4grp - ohi + n + w: the waves meet the diagonal and the start of the
+// window in the same step, and the steps between are the same straight-line
+// code for all of them.  A step's four key tiles are consecutive; each step
+// brings in one more tile, which streams global -> LDS by direct DMA into a
+// ring of NS slots two steps ahead (one raw barrier per step).  Chunks are
+// XOR-swizzled within each key row so the A-operand reads spread over the
+// LDS banks.  Each wave forms S^T = K^ Q^T on MFMA for its tile and votes
+// whether any in-window pair passes the trim-and-square threshold; live bits
+// are ORed into the bitmap (cleared by prep_k_kernel), so items that share a
+// bitmap word need no ordering.
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void fwd_screen_kernel(FwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   using G = ScreenTile<T, DP>;
-  constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NST = G::NST;
-  __shared__ __attribute__((aligned(16))) char ring[NST * G::TILEB];
+  constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NS = G::NS;
+  __shared__ __attribute__((aligned(16))) char ring[NS * G::TILEB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
   const int half = lane >> 5, l32 = lane & 31;
+  const int nkt = (int)(a.Tk_pad / kTile);
   // this block's lane: (XCD p % 8, engine (p >> 3) % 4); it runs the lane's
   // items at positions p >> 5, (p >> 5) + K, ... (K blocks per lane), which
   // are sorted longest first and end with empty entries
@@ -389,7 +410,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   for (int pos = p >> 5; pos < a.plan.kmax; pos += kstride) {
   const ScreenItem item = lane_items[pos];
   if (item.bh < 0) break;  // block-uniform: past this lane's items
-  const int bh = item.bh, grp = item.grp, slo = item.lo, shi = item.hi;
+  const int bh = item.bh, grp = item.grp, olo = item.lo, ohi = item.hi;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
   const HeadParams hp = head_params(a.r, a.w, h, causal);
@@ -426,14 +447,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int row = c / G::CPR, pc = c % G::CPR;
     goff[u] = (uint32_t)(row * G::ROWB + ((pc ^ G::swz(row)) << 4));
   }
-  // ring slot of the n-th tile of a segment: n % NST
-  auto issue = [&](int kt, int slot_idx) {
+  // The item's tiles in step order: tile number u is key tile A0 + u (wave w
+  // reads number n + w in step n) and sits in ring slot u % NS.  Numbers
+  // outside the key tiles any wave reads load a clamped tile instead (their
+  // slot is never read), so every step waits for the same count.
+  const int nsteps = ohi - olo + 1, A0 = grp * 4 - ohi;
+  int tmin = A0 < 0 ? 0 : A0, tmax = A0 + nsteps + 2 < nkt - 1 ? A0 + nsteps + 2 : nkt - 1;
+  if (tmin > nkt - 1) tmin = nkt - 1;
+  if (tmax < tmin) tmax = tmin;
+  auto issue = [&](int u, int slot_idx) {
+    int kt = A0 + u;
+    kt = kt < tmin ? tmin : (kt > tmax ? tmax : kt);
     const char* tb = kg + (int64_t)kt * G::TILEB;
 #pragma unroll
-    for (int u = 0; u < G::CPT; ++u)
+    for (int c = 0; c < G::CPT; ++c)
       __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(tb + goff[u]),
-          (void __attribute__((address_space(3)))*)(ring + slot_idx * G::TILEB + (u * 256 + wave * 64) * 16), 16, 0,
+          (const void __attribute__((address_space(1)))*)(tb + goff[c]),
+          (void __attribute__((address_space(3)))*)(ring + slot_idx * G::TILEB + (c * 256 + wave * 64) * 16), 16, 0,
           0);
   };
   // A-operand rows of key half kh: row 32kh + perm_row(l32), 16-byte chunk
@@ -498,15 +528,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     return lv;
   };
-  // Tile kt lies wholly inside the window of each of this wave's pairs iff
-  // i - j stays in window at its two extreme corners.
-  auto interior_tile = [&](int kt) {
-    const int d_max = q0 + 63 - kt * kTile, d_min = q0 - kt * kTile - 63;
-    return in_window(d_max, hp) && in_window(d_min, hp);
-  };
   // Live tiles are rare (a few percent of the window): one lane ORs the bits
   // of tile kd's live units into the bitmap (cleared by prep_k_kernel), so
-  // segments that share a bitmap word need no ordering.  v0, v1: the votes
+  // items that share a bitmap word need no ordering.  v0, v1: the votes
   // of key halves 0 and 1 (bit qh per lane).
   auto finish = [&](int kd, int v0, int v1) {
     const int vv = v0 | (v1 << 2);
@@ -520,11 +544,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   };
 
-  // Tiles past the item's last tile shi are replaced by shi itself: the ring
-  // slot they fill is free and never read, and every step then waits for the
-  // same count.
+  // Offsets [fa, fb] at which every wave of the group is valid, holds its tile
+  // in its key range, and the tile lies wholly inside every pair's window
+  // (distances 64o-63 .. 64o+63 inside [-wsh, wlim-1-wsh]): the straight-line
+  // step.  Block-uniform, from the four query tiles' key ranges.
+  int fa = olo, fb = ohi;
+  {
+    const int dl = -hp.wsh, du = (int)hp.wlim - 1 - hp.wsh;
+    const int ia = ceil_tiles(dl + 63), ib = floor_tiles(du - 63);
+    fa = fa > ia ? fa : ia;
+    fb = fb < ib ? fb : ib;
+    for (int w = 0; w < 4; ++w) {
+      const int qw = grp * 4 + w;
+      if (qw >= a.nqt) { fa = 1; fb = 0; break; }
+      int lw, hw;
+      key_tile_range(a, hp, causal, (int64_t)qw * kTile,
+                     (int64_t)qw * kTile + 63 < a.Tq - 1 ? (int64_t)qw * kTile + 63 : a.Tq - 1, lw, hw);
+      if (hw < lw) { fa = 1; fb = 0; break; }
+      fa = fa > qw - hw ? fa : qw - hw;
+      fb = fb < qw - lw ? fb : qw - lw;
+    }
+  }
+  // the first straight-line offset is taken by the general step, so each
+  // straight-line step's predecessor is one as well
+  const int n_fast0 = fa <= fb - 1 ? ohi - (fb - 1) : nsteps;  // steps [n_fast0, n_fast1)
+  const int n_fast1 = fa <= fb - 1 ? ohi - fa + 1 : nsteps;
+
 #pragma unroll
-  for (int n = 0; n < NST - 1; ++n) issue(slo + n <= shi ? slo + n : shi, n);
+  for (int u = 0; u < NS - 1; ++u) issue(u, u);
 #pragma unroll
   for (int qh = 0; qh < 2; ++qh) {
     iq[qh] = qrow[qh].inv_norm(a.eps);
@@ -535,71 +582,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   {
     // Software pipeline over the two 32-key halves of each tile: the vote on
     // one half runs while the MFMAs of the next half are in flight.  Order in
-    // step kt: MFMA(kt, keys 0-31) -> finish tile kt-1 (vote on its keys
-    // 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).  Tile kt sits
-    // in ring slot (kt - slo) % NST.
+    // step n (this wave's tile kt): MFMA(kt, keys 0-31) -> finish tile kt-1
+    // (vote on its keys 32-63) -> MFMA(kt, keys 32-63) -> vote(kt, keys 0-31).
     f32x16 acc0[2], acc1[2];
     bool pend = false, pint = false;  // tile kt-1: keys 32-63 pending in acc1
     int live0 = 0;                    // tile kt-1: vote on keys 0-31
     int pk0 = 0;
-    auto enter = [&](int kt) -> const char* {
-      // tile kt's DMA (own part) is complete once only the two younger tiles'
-      // chunks are outstanding; the barrier then covers all waves
-      wait_vmcnt<2 * G::CPT>();
+    int rslot = wave, dslot = NS - 1;  // this wave's read slot, the DMA slot
+    // Step n reads numbers n .. n+3 (landed once at most NS-5 younger tiles
+    // are outstanding; the barrier covers all waves) and refills the slot of
+    // number n-1, which the previous step read last.
+    auto enter = [&](int n) -> const char* {
+      wait_vmcnt<(NS - 5) * G::CPT>();
       __builtin_amdgcn_s_barrier();
-      const int n = kt - slo;
-      issue(kt + NST - 1 <= shi ? kt + NST - 1 : shi, (n + NST - 1) & (NST - 1));
-      return ring + (n & (NST - 1)) * G::TILEB;
+      issue(n + NS - 1, dslot);
+      const char* slot = ring + rslot * G::TILEB;
+      rslot = rslot + 1 == NS ? 0 : rslot + 1;
+      dslot = dslot + 1 == NS ? 0 : dslot + 1;
+      return slot;
     };
-    // General step: tiles at the window's edges, or outside some wave's window.
-    auto step = [&](int kt) {
-      const char* slot = enter(kt);
+    // General step: offsets at the window's edges, or where some wave's tile
+    // is outside its key range.
+    auto step = [&](int n) {
+      const char* slot = enter(n);
+      const int o = ohi - n, kt = A0 + n + wave;
       const bool mine = kt >= kt_lo && kt <= kt_hi;
       if (mine) half_mma(slot, 0, acc0);
-      if (kt > slo && pend) finish(kt - 1, live0, vote_half(acc1, pk0, 1, pint));
+      if (n > 0 && pend) finish(kt - 1, live0, vote_half(acc1, pk0, 1, pint));
       if (mine) {
         half_mma(slot, 1, acc1);
-        pint = interior_tile(kt);
+        pint = in_window(kTile * o + 63, hp) && in_window(kTile * o - 63, hp);
         live0 = vote_half(acc0, kt * kTile, 0, pint);
         pk0 = kt * kTile;
       }
       pend = mine;
     };
-    // Straight-line step for tiles wholly inside every valid wave's window,
-    // whose predecessor kt-1 was one as well: plain maxima, no branches but
-    // the rare live-tile store.  A wave past the last query tile has zero
-    // query rows, so its votes fail.
-    auto step_inside = [&](int kt) {
-      const char* slot = enter(kt);
+    // Straight-line step: every wave's tile is in its range and wholly inside
+    // the window, and so was the previous one: plain maxima, no branches but
+    // the rare live-tile store.
+    auto step_inside = [&](int n) {
+      const char* slot = enter(n);
+      const int kt = A0 + n + wave;
       half_mma(slot, 0, acc0);
-      finish(kt - 1, pend ? live0 : 0, pend ? vote_half(acc1, 0, 1, true) : 0);
+      finish(kt - 1, live0, vote_half(acc1, 0, 1, true));
       half_mma(slot, 1, acc1);
       live0 = vote_half(acc0, 0, 0, true);
       pend = true;
       pint = true;
       pk0 = kt * kTile;
     };
-    // Tiles [ia, ib] lie inside the window of every valid wave of the block:
-    // from the last valid wave's first interior tile to the first wave's last.
-    int ia, ib;
-    {
-      const int last = (a.nqt - 1 - grp * 4 < 3 ? a.nqt - 1 - grp * 4 : 3);
-      const int64_t qa = (int64_t)(grp * 4 + last) * kTile, qb = (int64_t)grp * 4 * kTile;
-      auto fdiv = [](int64_t x) { return (int)(x >= 0 ? x / kTile : -((-x + kTile - 1) / kTile)); };
-      ia = fdiv(qa + 2 * kTile - 1 - hp.wc);                                   // d_max = qa + 63 - k0 < wc
-      ib = causal ? (int)(qb / kTile) - 1 : fdiv(qb - kTile + (int64_t)hp.wc);  // d_min >= 0, or > -wc
-      if (ia < slo) ia = slo;
-      if (ib > shi) ib = shi;
-    }
-    int kt = slo;
-    if (ia < ib) {
-      for (; kt <= ia; ++kt) step(kt);
-      for (; kt <= ib; ++kt) step_inside(kt);
-    }
-    for (; kt <= shi; ++kt) step(kt);
-    if (pend) finish(shi, live0, vote_half(acc1, pk0, 1, pint));
-    // the trailing replacement loads have landed and every wave is done with
-    // the ring before the next item refills it
+    int n = 0;
+    for (; n < n_fast0; ++n) step(n);
+    for (; n < n_fast1; ++n) step_inside(n);
+    for (; n < nsteps; ++n) step(n);
+    if (pend) finish(A0 + nsteps - 1 + wave, live0, vote_half(acc1, pk0, 1, pint));
+    // the trailing loads have landed and every wave is done with the ring
+    // before the next item refills it
     wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
   }
