@@ -213,10 +213,10 @@ struct HeadParams {
 // and wc <= 2^30, so dd + wsh never overflows.  A window that is not a number
 // (or not positive) is empty: wc = 0, limit 0, so no pair of the head is live
 // and its outputs are zero (the reference's dense path gives NaN there).
-__device__ inline HeadParams head_params(const float* r, const float* w, int h, bool causal) {
+__device__ inline HeadParams head_params_rw(float r, float w, bool causal) {
   HeadParams p;
-  p.r = r[h];
-  p.w = w[h];
+  p.r = r;
+  p.w = w;
   p.iw = 1.0f / p.w;
   const float c = ceilf(p.w);
   p.wc = !(c > 0.0f) ? 0 : (c > 1073741824.0f ? 1073741824 : (int)c);
@@ -224,6 +224,9 @@ __device__ inline HeadParams head_params(const float* r, const float* w, int h, 
   p.wsh = causal ? 0 : p.wc - 1;
   p.wlim = p.wc == 0 ? 0u : (causal ? (unsigned)p.wc : (unsigned)(2 * p.wc - 1));
   return p;
+}
+__device__ inline HeadParams head_params(const float* r, const float* w, int h, bool causal) {
+  return head_params_rw(r[h], w[h], causal);
 }
 
 // Wave-uniform mask of the registers r of a C block for which some lane has

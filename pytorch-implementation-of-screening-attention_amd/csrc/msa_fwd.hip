@@ -50,6 +50,8 @@ namespace msa {
 constexpr int kScreenBlocksPerLane = 256;
 struct ScreenItem {
   int bh, grp, lo, hi;  // head, 4-query-tile group, tile offsets qt - kt in [lo, hi]
+  float r, w;           // the head's r_h, w_h (copied, so one load gives the screen all)
+  int pad[2];
 };
 struct ScreenPlan {
   ScreenItem* table;  // [8 XCDs][4 engine lanes][kmax]
@@ -174,7 +176,7 @@ __device__ inline void plan_deal(int i, int nl, int& e, int& j) {
 // engine L / 8).
 __device__ void screen_plan(const PrepKArgs& a, int x) {
   __shared__ int heads[kPlanMaxHeads], wcs[kPlanMaxHeads];
-  __shared__ float keys[kPlanMaxRanked];
+  __shared__ float keys[kPlanMaxRanked], rh[kPlanMaxRanked], wh[kPlanMaxRanked];
   __shared__ int wch[kPlanMaxRanked];
   __shared__ int hist[257], start[257];
   __shared__ int total;
@@ -192,6 +194,8 @@ __device__ void screen_plan(const PrepKArgs& a, int x) {
       const float wf = a.w[h];
       keys[h] = window_rank_key(wf);
       wch[h] = plan_wc(wf);
+      rh[h] = a.r[h];
+      wh[h] = wf;
     }
   __syncthreads();
   if (per_xcd) {
@@ -240,14 +244,16 @@ __device__ void screen_plan(const PrepKArgs& a, int x) {
     const int pos = atomicAdd(&start[hi - lo + 1], 1);
     int e, j;
     plan_deal(pos, nl, e, j);
-    if (j < kmax) lane_base(e)[j] = ScreenItem{bh, grp, lo, hi};  // j < kmax always (kmax bounds the items)
+    const int h = bh % a.H;
+    const float r = small_h ? rh[h] : a.r[h], w = small_h ? wh[h] : a.w[h];
+    if (j < kmax) lane_base(e)[j] = ScreenItem{bh, grp, lo, hi, r, w, {0, 0}};  // j < kmax always (kmax bounds the items)
   });
   // positions past each lane's items: empty
   const int n = total, full = n / nl, r = n - full * nl;
   for (int e = 0; e < nl; ++e) {
     const bool extra = r > 0 && ((full & 1) ? e >= nl - r : e < r);
     ScreenItem* lb = lane_base(e);
-    for (int j = full + (extra ? 1 : 0) + t; j < kmax; j += blockDim.x) lb[j] = ScreenItem{-1, 0, 0, -1};
+    for (int j = full + (extra ? 1 : 0) + t; j < kmax; j += blockDim.x) lb[j] = ScreenItem{-1, 0, 0, -1, 0.0f, 0.0f, {0, 0}};
   }
 }
 
@@ -408,22 +414,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const ScreenItem* lane_items = a.plan.table + ((p & 7) * 4 + ((p >> 3) & 3)) * a.plan.kmax;
   const int kstride = (int)(gridDim.x >> 5);
   for (int pos = p >> 5; pos < a.plan.kmax; pos += kstride) {
-  const ScreenItem item = lane_items[pos];
-  if (item.bh < 0) break;  // block-uniform: past this lane's items
-  const int bh = item.bh, grp = item.grp, olo = item.lo, ohi = item.hi;
+  // the whole entry in one round trip (the asm keeps the compiler from
+  // splitting the loads at the test)
+  const int4 item = *(const int4*)(lane_items + pos);
+  const float4 irw = *((const float4*)(lane_items + pos) + 1);
+  asm volatile("" ::"v"(item.x), "v"(item.y), "v"(item.z), "v"(item.w), "v"(irw.x), "v"(irw.y));
+  if (item.x < 0) break;  // block-uniform: past this lane's items
+  const int bh = item.x, grp = item.y, olo = item.z, ohi = item.w;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
-  const HeadParams hp = head_params(a.r, a.w, h, causal);
   const int qt = grp * 4 + wave;
   const bool wave_ok = qt < a.nqt;
   const int q0 = qt * kTile;
 
-  int kt_lo, kt_hi;
-  key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
-  if (!wave_ok) { kt_lo = 0; kt_hi = -1; }
-
-  // own query rows (raw B operands); their 1/|q| is formed once the first
-  // key tiles' DMA is in flight behind them
+  // The own query rows (raw B operands) and the first key tiles' DMA need
+  // only the item: they are issued first, and the head parameters and tile
+  // ranges are formed while they are in flight.
   PRow<T, DP> qrow[2];
 #pragma unroll
   for (int qh = 0; qh < 2; ++qh) {
@@ -431,6 +437,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const bool ok = wave_ok && i < a.Tq;
     qrow[qh].load((const T*)a.q + b * a.qs.sb + (int64_t)(ok ? i : 0) * a.qs.st + h * a.qs.sh, ok, a.D, half);
   }
+  __builtin_amdgcn_sched_barrier(0);  // query loads issue before the DMA
   frag qf[2 * NKS];
   float iq[2];
   // bitmap rows of the wave's two query units (32 queries each)
@@ -466,6 +473,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
           (void __attribute__((address_space(3)))*)(ring + slot_idx * G::TILEB + (c * 256 + wave * 64) * 16), 16, 0,
           0);
   };
+#pragma unroll
+  for (int u = 0; u < NS - 1; ++u) issue(u, u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const HeadParams hp = head_params_rw(irw.x, irw.y, causal);
+  int kt_lo, kt_hi;
+  key_tile_range(a, hp, causal, q0, q0 + 63 < a.Tq - 1 ? q0 + 63 : a.Tq - 1, kt_lo, kt_hi);
+  if (!wave_ok) { kt_lo = 0; kt_hi = -1; }
+
   // A-operand rows of key half kh: row 32kh + perm_row(l32), 16-byte chunk
   // (KS*ks + PER*half)*sizeof(T)/16 = ks*KS*sizeof(T)/16 + half*PER*sizeof(T)/16
   uint32_t aoff[2][NKS];
@@ -570,8 +586,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int n_fast0 = fa <= fb - 1 ? ohi - (fb - 1) : nsteps;  // steps [n_fast0, n_fast1)
   const int n_fast1 = fa <= fb - 1 ? ohi - fa + 1 : nsteps;
 
-#pragma unroll
-  for (int u = 0; u < NS - 1; ++u) issue(u, u);
 #pragma unroll
   for (int qh = 0; qh < 2; ++qh) {
     iq[qh] = qrow[qh].inv_norm(a.eps);

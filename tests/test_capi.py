@@ -34,16 +34,16 @@ def test_version_and_sizes():
     L = _native.lib()
     assert L.msa_version() == (0 << 16) | (1 << 8)
     # B=4, T=8192, H=8, D=64 bf16: one normalised K^ copy, then the screen's
-    # work-plan table: 32 lanes x kmax entries of 16 bytes (kmax = 68 here:
-    # 4 heads per XCD x 68 items of at most 40 key tiles, over 4 lanes)
+    # work-plan table: 32 lanes x kmax entries of 32 bytes (kmax = 68 here:
+    # 4 heads per XCD x 68 items of at most 40 steps, over 4 lanes)
     one = 4 * 8 * 8192 * 64 * 2
-    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == one + 32 * 68 * 16
+    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == one + 32 * 68 * 32
     # 2*nqt query-unit rows of ceil(2*nkt/32) words per (b, h)
     assert L.msa_tile_bits_words(4, 8, 8192, 8192) == 4 * 8 * 256 * 8
     assert L.msa_tile_bits_words(1, 1, 65, 65) == 4
     assert L.msa_tile_bits_words(1, 1, 64, 1100) == 2 * 2
     # D=16 is padded to 32 in the workspace; one head, one item per lane at most
-    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4 + 512
+    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4 + 1024
     # backward workspace: (dr, dw) partial per (b, h, 32-key unit), then dh
     # (b, h, Tq_pad, DP) in the input type and 1/|q| (b, h, Tq_pad) fp32, each
     # 256-byte aligned
