@@ -12,6 +12,12 @@ headline one (which test_gpu_parity covers):
     the 6-layer LM: 256 greedy steps, each step's logits against a full
     forward() over the finished sequence.
 
+The configurations exactly as BASELINE.json states them (the module's own
+initialisation: r = 2, windows 2..256) are checked too: the training step
+against the explicit-matrix core, and the literal decode against the
+explicit-matrix core run on the last 2,048 positions only (every window is
+below 263 in bf16, so six layers see at most 6 x 263 positions back).
+
 Tolerances are the north star's (max|got-ref|/max|ref| per tensor): 1e-5 in
 fp32 and 2e-2 in bf16.
 """
@@ -81,13 +87,13 @@ def _zipf_ids(B, T, s, seed):
     return ids.view(B, T)
 
 
-def _dense_core(attn):
-    """attn.core with the explicit-matrix form, computed in float32."""
+def _dense_core(attn, dtype=torch.float32):
+    """attn.core with the explicit-matrix form, computed in `dtype`."""
     from multiscreen._dense import screening_core_dense
 
     def core(q, k, v, key_padding_mask=None):
-        y = screening_core_dense(q.float(), k.float(), v.float(), attn.sharpness().float(),
-                                 attn.window().float(), attn.causal, attn.eps, key_padding_mask)
+        y = screening_core_dense(q.to(dtype), k.to(dtype), v.to(dtype), attn.sharpness().to(dtype),
+                                 attn.window().to(dtype), attn.causal, attn.eps, key_padding_mask)
         return y.to(q.dtype)
     return core
 
@@ -160,6 +166,73 @@ def test_cfg5_decode_100k_cache_matches_full_forward():
         for blk in lm.blocks:
             x = blk(x)
         ref = lm._head(x[:, CAP - STEPS - 1:CAP - 1]).float()
+    torch.cuda.synchronize()
+    got = torch.stack(steps, dim=1)
+    assert got.shape == ref.shape
+    assert _t_rel(got, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,B", [(torch.float32, 2), (torch.bfloat16, 8)], ids=["f32", "bf16"])
+def test_cfg3_literal_init_training_step_matches_dense_core(dtype, B):
+    # The module's own init (r = 2, windows 2..256): few pairs pass at init,
+    # but the wide heads of every layer have some.  The fp32 reference core
+    # runs in float64, so only this path's rounding is measured.  Each head's
+    # s_r / s_v gradient is then a sum over a handful of live pairs of both
+    # signs (1e-9 .. 1e-6), so those are compared as one tensor per kind over
+    # all six layers (max|got-ref| / max|ref| over the 48 values).
+    lm = _lm(2048, dtype)
+    ids = _zipf_ids(B, 2048, 1.1, seed=3).to(DEV)
+    loss, logits, grads = _train_step(lm, ids)
+    assert math.isfinite(loss.item())
+    live_heads = sum(int((grads[f"blocks.{i}.attn.s_r"] != 0).sum().item()) for i in range(6))
+    assert live_heads > 0
+    ref_dtype = torch.float64 if dtype == torch.float32 else torch.float32
+    for blk in lm.blocks:
+        blk.attn.core = _dense_core(blk.attn, ref_dtype)
+    loss_r, logits_r, grads_r = _train_step(lm, ids)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert abs(loss.item() - loss_r.item()) <= tol * abs(loss_r.item())
+    assert _t_rel(logits, logits_r) <= tol
+    for kind in ("s_r", "s_v"):
+        names = [f"blocks.{i}.attn.{kind}" for i in range(6)]
+        got = torch.stack([grads[n] for n in names])
+        ref = torch.stack([grads_r[n] for n in names])
+        assert ref.abs().max().item() > 0, kind
+        assert _t_rel(got, ref) <= tol, kind
+    for name, gr in grads_r.items():
+        if name.endswith(("attn.s_r", "attn.s_v")):
+            continue
+        assert gr.abs().max().item() > 0, name
+        assert _t_rel(grads[name], gr) <= tol, name
+
+
+def test_cfg5_literal_decode_matches_dense_core_on_suffix():
+    B, CAP, STEPS, SUFFIX = 16, 100000, 256, 2048
+    lm = _lm(CAP, torch.bfloat16).eval()  # the module's own init: windows 2..256 (bf16: ~261)
+    wmax = max(float(blk.attn.window().detach().float().max()) for blk in lm.blocks)
+    assert 6 * math.ceil(wmax) + STEPS + 1 <= SUFFIX  # the suffix holds the dependency cone
+    g = torch.Generator().manual_seed(7)
+    prompt = torch.randint(0, VOCAB, (B, CAP - STEPS), generator=g).to(DEV)
+    caches = lm.new_cache(B, CAP, torch.bfloat16, DEV)
+    with torch.no_grad():
+        logits = lm.prefill(prompt, caches)
+        steps, toks = [logits.float()], []
+        for s in range(STEPS):
+            tok = logits.argmax(-1, keepdim=True)
+            toks.append(tok)
+            if s + 1 < STEPS:
+                logits = lm.decode_step(tok, caches, CAP - STEPS + s)
+                steps.append(logits.float())
+        seq = torch.cat([prompt] + toks, dim=1)
+        # reference: the explicit-matrix core on the last SUFFIX positions, with
+        # their true positions; position t depends on t-6*ceil(wmax) .. t only
+        for blk in lm.blocks:
+            blk.attn.core = _dense_core(blk.attn)
+        s0 = CAP - SUFFIX
+        x = lm.embed(seq[:, s0:], start=s0)
+        for blk in lm.blocks:
+            x = blk(x)
+        ref = lm._head(x[:, SUFFIX - STEPS - 1:SUFFIX - 1]).float()
     torch.cuda.synchronize()
     got = torch.stack(steps, dim=1)
     assert got.shape == ref.shape
