@@ -181,10 +181,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
   __shared__ typename Mma<T>::frag qh[2 * (DP / Mma<T>::KS)][kWave];  // own raw q, dh operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
-  xcd_interleave_ranked(a.w, a.H, qu, bh);
+  float head_r, head_w;
+  xcd_interleave_ranked(a.r, a.w, a.H, qu, bh, head_r, head_w);
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
-  const HeadParams hp = head_params(a.r, a.w, h, causal);
+  const HeadParams hp = head_params_rw(head_r, head_w, causal);
   const int i = qu * kUnit + l32;
   const bool valid = i < a.Tq;
   const int ii = valid ? i : 0;
@@ -428,13 +429,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   __shared__ typename Mma<T>::frag kvs[2 * (DP / Mma<T>::KS)][kWave];  // own raw k, v operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int ku, bh;
-  xcd_interleave_ranked(a.w, a.H, ku, bh);
+  float head_r, head_w;
+  xcd_interleave_ranked(a.r, a.w, a.H, ku, bh, head_r, head_w);
   // a key unit's live query units lie after it (its window runs forward), so
   // under a causal mask the lowest key units carry the most work: they go first
   if (a.causal) ku = (int)gridDim.x - 1 - ku;
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
-  const HeadParams hp = head_params(a.r, a.w, h, causal);
+  const HeadParams hp = head_params_rw(head_r, head_w, causal);
   const int k0 = ku * kUnit;
   const int j = k0 + l32;
   const bool jvalid = j < a.Tk;

@@ -621,25 +621,33 @@ __device__ inline void xcd_interleave(int& bx, int& by) {
 // Ranks come from a total order, (window key, head index) with a NaN window
 // keyed as +inf, so the ranks 0..H-1 are a permutation of the heads whatever
 // the windows hold (NaN, infinities, duplicates): every (b, h) gets exactly
-// one block row.  head_rank_select() returns the head of rank r.
+// one block row.  The mapping also returns the selected head's r_h and w_h:
+// lane o loads r[o] and w[o] in the one round trip the ranking needs, and the
+// head's values come back by readlane (no second dependent load).
 __device__ inline float window_rank_key(float w) { return w != w ? INFINITY : w; }
-__device__ inline int head_rank_select(const float* w, int H, int r) {
+__device__ inline void xcd_interleave_ranked(const float* r, const float* w, int H, int& bx, int& by, float& rh,
+                                             float& wh) {
+  xcd_interleave(bx, by);
+  const int BH = (int)gridDim.y;
+  if (H > 64 || BH % H != 0) {
+    rh = r[by % H];
+    wh = w[by % H];
+    return;
+  }
   const int lane = threadIdx.x & 63;
-  const float wl = window_rank_key(lane < H ? w[lane] : 0.0f);  // lane o holds head o's key
+  const float wraw = lane < H ? w[lane] : 0.0f, rraw = lane < H ? r[lane] : 0.0f;
+  const float wl = window_rank_key(wraw);  // lane o holds head o's key
+  const int B = BH / H, rk = by / B, b = by % B;
   int rank = 0;
   for (int o = 0; o < H; ++o) {
     const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), o));
     rank += (wo > wl || (wo == wl && o < lane)) ? 1 : 0;
   }
-  const unsigned long long sel = __ballot(lane < H && rank == r);
-  return sel != 0ull ? (int)__builtin_ctzll(sel) : r;  // sel is never empty: ranks are a permutation
-}
-__device__ inline void xcd_interleave_ranked(const float* w, int H, int& bx, int& by) {
-  xcd_interleave(bx, by);
-  const int BH = (int)gridDim.y;
-  if (H > 64 || BH % H != 0) return;
-  const int B = BH / H, r = by / B, b = by % B;
-  by = b * H + head_rank_select(w, H, r);
+  const unsigned long long sel = __ballot(lane < H && rank == rk);
+  const int h = sel != 0ull ? (int)__builtin_ctzll(sel) : rk;  // sel is never empty: ranks are a permutation
+  by = b * H + h;
+  rh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rraw), h));
+  wh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wraw), h));
 }
 
 // XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs

@@ -681,10 +681,11 @@ void fwd_live_kernel(FwdKArgs a) {
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
-  xcd_interleave_ranked(a.w, a.H, qu, bh);
+  float head_r, head_w;
+  xcd_interleave_ranked(a.r, a.w, a.H, qu, bh, head_r, head_w);
   const int b = bh / a.H, h = bh % a.H;
   const bool causal = a.causal != 0;
-  const HeadParams hp = head_params(a.r, a.w, h, causal);
+  const HeadParams hp = head_params_rw(head_r, head_w, causal);
   const int i = qu * kUnit + l32;
   const bool valid = i < a.Tq;
   // output row of query i (formed where it is stored, so nothing holds it
