@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   }
   __builtin_amdgcn_sched_barrier(0);  // query loads issue before the DMA
   frag qf[2 * NKS];
-  float iq[2];
+  float qthr[2];  // vote threshold on acc for this lane's query of unit qh
   // bitmap rows of the wave's two query units (32 queries each)
   uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + 2 * (wave_ok ? qt : 0)) * a.nku_words;
 
@@ -516,15 +516,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma(kf[ks], qf[qh * NKS + ks], acc[qh]);
     }
   };
-  // Threshold vote on key half kh of the tile at k0, per lane (no ballot): a(s)
-  // is monotone in s and s = acc/|q_i|, so a 32x32 unit has a live pair iff
-  // its largest in-window acc passes.  Register r of the half holds key
-  // k0 + 32kh + 16(r/8) + 8half + r%8.  Tiles wholly inside every pair's
-  // window skip the per-register window test; in the other tiles each 32x32
-  // unit is classed by its distance range c-31 .. c+31 (the window is one
-  // interval of distances): wholly inside (plain maximum), wholly outside (no
-  // vote) or cut by a window edge (per-register test).  Bit qh of the result:
-  // this lane's query of unit qh passes.
+  // Threshold vote on key half kh of the tile at k0: a(s) is monotone in s and
+  // s = acc/|q_i|, so a 32x32 unit has a live pair iff its largest in-window
+  // acc exceeds (1 - 1/r)|q_i|.  The vote compares with qthr (the head's
+  // conservative gate times |q_i|), so a unit within 1e-6 below the threshold
+  // may be marked too; the live pass's exact test gives its pairs alpha = 0.
+  // The compare's lane mask is the wave's vote, so the result is
+  // wave-uniform: bit qh set iff unit (qh, kh) has a passing pair.  Register r
+  // of the half holds key k0 + 32kh + 16(r/8) + 8half + r%8.  Tiles wholly
+  // inside every pair's window skip the per-register window test; in the
+  // other tiles each 32x32 unit is classed by its distance range c-31 .. c+31
+  // (the window is one interval of distances): wholly inside (plain maximum),
+  // wholly outside (no vote) or cut by a window edge (per-register test).
   auto vote_half = [&](const f32x16 (&acc)[2], int k0, int kh, bool interior) -> int {
     int lv = 0;
 #pragma unroll
@@ -540,20 +543,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         for (int r = 0; r < 16; ++r)
           mx = fmaxf(mx, in_window(rel0 - (16 * (r >> 3) + (r & 7)), hp) ? acc[qh][r] : -INFINITY);
       }
-      lv |= (trim(mx * iq[qh], hp.r) > 0.0f ? 1 : 0) << qh;
+      lv |= (__ballot(mx > qthr[qh]) != 0ull ? 1 : 0) << qh;
     }
     return lv;
   };
   // Live tiles are rare (a few percent of the window): one lane ORs the bits
   // of tile kd's live units into the bitmap (cleared by prep_k_kernel), so
   // items that share a bitmap word need no ordering.  v0, v1: the votes
-  // of key halves 0 and 1 (bit qh per lane).
+  // of key halves 0 and 1 (bit qh, wave-uniform).
   auto finish = [&](int kd, int v0, int v1) {
-    const int vv = v0 | (v1 << 2);
-    if (__ballot(vv != 0) != 0 && wave_ok) {
+    if ((v0 | v1) != 0 && wave_ok) {
       // row qh, key units 2kd (bit 0) and 2kd + 1 (bit 1): one word
-      const uint32_t m0 = (__ballot(vv & 1) != 0 ? 1u : 0u) | (__ballot(vv & 4) != 0 ? 2u : 0u);
-      const uint32_t m1 = (__ballot(vv & 2) != 0 ? 1u : 0u) | (__ballot(vv & 8) != 0 ? 2u : 0u);
+      const uint32_t m0 = (uint32_t)((v0 & 1) | ((v1 & 1) << 1));
+      const uint32_t m1 = (uint32_t)(((v0 >> 1) & 1) | (((v1 >> 1) & 1) << 1));
       const int u = 2 * kd;
       if (lane == 0 && m0 != 0u) atomicOr(&brow[u >> 5], m0 << (u & 31));
       if (lane == 0 && m1 != 0u) atomicOr(&brow[a.nku_words + (u >> 5)], m1 << (u & 31));
@@ -586,9 +588,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int n_fast0 = fa <= fb - 1 ? ohi - (fb - 1) : nsteps;  // steps [n_fast0, n_fast1)
   const int n_fast1 = fa <= fb - 1 ? ohi - fa + 1 : nsteps;
 
+  // s = acc/max(|q|, eps) passes the gate iff acc > thr max(|q|, eps); a gate
+  // at or below 0 (r at most 1 + 1e-6) is taken as 0, the exact threshold of r = 1
 #pragma unroll
   for (int qh = 0; qh < 2; ++qh) {
-    iq[qh] = qrow[qh].inv_norm(a.eps);
+    qthr[qh] = fmaxf(hp.thr, 0.0f) / qrow[qh].inv_norm(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = qrow[qh].f[ks];
   }
