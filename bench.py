@@ -18,7 +18,8 @@ Also reported:
                        and the attention kernels' share of it
   cfg4_prefill_100k    configs[3]: the T=100,000 prefill forward, with its
                        algorithmic flop C(|W|+|A|) and bf16-peak fraction
-  cfg5_decode_literal  configs[4] as written: ms per generated token
+  cfg5_decode_literal  configs[4] as written: ms per generated token, eager
+                       and replayed from a captured HIP graph (same tokens)
 Prints ONE JSON line.
 """
 
@@ -326,17 +327,37 @@ def cfg5_bench(torch, new_tokens=256):
         tok = logits.argmax(-1, keepdim=True)
         for s in range(4):  # untimed warm-up of the decode path (positions overwritten below)
             lm.decode_step(tok, caches, CAP - new_tokens + s)
+        first = tok
+        toks = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for s in range(new_tokens - 1):
             logits = lm.decode_step(tok, caches, CAP - new_tokens + s)
             tok = logits.argmax(-1, keepdim=True)
+            toks.append(tok)
         torch.cuda.synchronize()
         t_dec = time.perf_counter() - t0
+        # the same 255 steps again, each one replay of a captured HIP graph
+        # (GraphDecoder: position and token on the device); same caches, same
+        # start, so the same tokens
+        from multiscreen.model import GraphDecoder
+        dec = GraphDecoder(lm, caches, first, CAP - new_tokens, new_tokens - 1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(new_tokens - 1):
+            dec.step()
+        torch.cuda.synchronize()
+        t_graph = time.perf_counter() - t0
+        same = bool(torch.equal(dec.tokens, torch.cat(toks, dim=1)))
     return {"workload": "configs[4]: MultiscreenLM 6 layers, B=16, bf16 KV cache 100000, init windows, "
                         "prefill + 256 greedy tokens",
             "prefill_s": round(t_prefill, 4), "ms_per_token": round(t_dec / (new_tokens - 1) * 1e3, 4),
-            "tokens_per_s": round(B * (new_tokens - 1) / t_dec, 1)}
+            "tokens_per_s": round(B * (new_tokens - 1) / t_dec, 1),
+            "ms_per_token_graph": round(t_graph / (new_tokens - 1) * 1e3, 4),
+            "tokens_per_s_graph": round(B * (new_tokens - 1) / t_graph, 1),
+            "graph_tokens_equal_eager": same,
+            "note": "ms_per_token: eager decode_step per token (launch-bound: about 120 kernel launches); "
+                    "ms_per_token_graph: the same steps replayed from one captured HIP graph"}
 
 
 def main():

@@ -153,9 +153,11 @@ size_t msa_decode_workspace_bytes(int B, int H, int D, int max_len);
  *   kcache, vcache : (B, Tcap, H, D) raw k/v projections, strides (sb, st, sh);
  *            cache_cap = Tcap, and 1 <= cache_len <= cache_cap.
  *   window_hint : 0, or a bound on ceil(w_h) over the heads that sizes the
- *            launch (one block per 2048-key chunk of each window).  Only the
- *            windowed keys are visited whatever its value; a wrong hint costs
- *            time, never correctness.
+ *            launch (one block per 2048-key chunk of each window; one block
+ *            per head and no workspace traffic when the windows fit one
+ *            chunk).  Only the windowed keys are visited whatever its value,
+ *            and every launch shape gives bitwise the same y: a wrong hint
+ *            costs time, never correctness.
  *   y      : (B, H, D) contiguous, TanhNorm(h).
  */
 int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
@@ -164,6 +166,23 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh,
                int B, int H, int D, int dtype, int cache_len, int cache_cap, int window_hint,
                const float* r, const float* w, float eps,
                void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * msa_decode with the cache length read on the device: last_pos points to
+ * the int64 position of the newest key (the query's), so the length is
+ * *last_pos + 1, clamped to [1, cache_cap].  No counterpart in the reference
+ * (its generate has no cache, model.py:111-141): it is for a decode step
+ * captured once in a HIP graph and replayed as the sequence grows, the
+ * position advanced on the device.  Workspace: msa_decode_workspace_bytes(B,
+ * H, D, cache_cap).  Otherwise the same arguments, checks and results as
+ * msa_decode.
+ */
+int msa_decode_at(const void* q, int64_t q_sb, int64_t q_sh,
+                  const void* kcache, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                  const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                  int B, int H, int D, int dtype, const int64_t* last_pos, int cache_cap, int window_hint,
+                  const float* r, const float* w, float eps,
+                  void* y, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * msa_decode without a workspace argument and without any allocation: the

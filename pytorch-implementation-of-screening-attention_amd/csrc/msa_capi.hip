@@ -288,13 +288,16 @@ size_t msa_decode_workspace_bytes(int B, int H, int D, int max_len) {
   return (size_t)B * H * msa::decode_max_chunks(max_len) * D * sizeof(float);
 }
 
-// Validates a decode call and fills c (all but the partial-sum buffer).
+// Validates a decode call and fills c (all but the partial-sum buffer).  The
+// cache length is cache_len, or, with last_pos non-null, read on the device
+// (*last_pos + 1, clamped to [1, cache_cap]; cache_len is then ignored).
 // Returns MSA_OK, an error code, or -1 when B == 0 (nothing to do).
 static int decode_setup(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
                         int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H,
-                        int D, int dtype, int cache_len, int cache_cap, int window_hint, const float* r,
-                        const float* w, float eps, void* y, void* stream, msa::DecodeCall* c) {
+                        int D, int dtype, int cache_len, const int64_t* last_pos, int cache_cap, int window_hint,
+                        const float* r, const float* w, float eps, void* y, void* stream, msa::DecodeCall* c) {
   msa::Geometry g;
+  if (last_pos != nullptr) cache_len = cache_cap;  // the longest the device length can be
   int rc = check_geometry(B, H, 1, cache_len, D, dtype, 1, &g);
   if (rc != MSA_OK) return rc;
   if (B == 0) return -1;
@@ -308,6 +311,7 @@ static int decode_setup(const void* q, int64_t q_sb, int64_t q_sh, const void* k
   if (r == nullptr || w == nullptr) return fail(MSA_ERR_INVALID, "r and w must be device arrays of H floats");
   if ((rc = check_out("y", y)) != MSA_OK) return rc;
   c->B = B; c->H = H; c->D = D; c->DP = g.DP; c->dtype = dtype; c->len = cache_len;
+  c->last_pos = last_pos; c->cap = cache_cap;
   c->q = q; c->q_sb = q_sb; c->q_sh = q_sh;
   c->kc = kcache; c->ks = {k_sb, k_st, k_sh};
   c->vc = vcache; c->vs = {v_sb, v_st, v_sh};
@@ -317,6 +321,8 @@ static int decode_setup(const void* q, int64_t q_sb, int64_t q_sh, const void* k
   // windows; any grid gives the same result, the hint only sizes it
   const int span = window_hint > 0 && window_hint < cache_len ? window_hint : cache_len;
   c->blocks = B * H * msa::decode_max_chunks(span);
+  // windows that fit one chunk: one block per head finishes it (same result)
+  c->single = span <= msa::decode_chunk_keys() ? 1 : 0;
   c->stream = (hipStream_t)stream;
   return MSA_OK;
 }
@@ -327,7 +333,7 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, in
                void* y, void* workspace, size_t workspace_bytes, void* stream) {
   msa::DecodeCall c;
   const int rc = decode_setup(q, q_sb, q_sh, kcache, k_sb, k_st, k_sh, vcache, v_sb, v_st, v_sh, B, H, D, dtype,
-                              cache_len, cache_cap, window_hint, r, w, eps, y, stream, &c);
+                              cache_len, nullptr, cache_cap, window_hint, r, w, eps, y, stream, &c);
   if (rc == -1) return ok();
   if (rc != MSA_OK) return rc;
   const size_t need = msa_decode_workspace_bytes(B, H, D, cache_len);
@@ -335,6 +341,23 @@ int msa_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, in
     return fail(MSA_ERR_WORKSPACE, "decode workspace holds %zu bytes, %zu needed", workspace_bytes, need);
   c.part = (float*)workspace;
   return hip_status(msa::launch_decode(c), "msa_decode launch");
+}
+
+int msa_decode_at(const void* q, int64_t q_sb, int64_t q_sh, const void* kcache, int64_t k_sb, int64_t k_st,
+                  int64_t k_sh, const void* vcache, int64_t v_sb, int64_t v_st, int64_t v_sh, int B, int H, int D,
+                  int dtype, const int64_t* last_pos, int cache_cap, int window_hint, const float* r, const float* w,
+                  float eps, void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  if (last_pos == nullptr) return fail(MSA_ERR_INVALID, "last_pos must be a device int64");
+  msa::DecodeCall c;
+  const int rc = decode_setup(q, q_sb, q_sh, kcache, k_sb, k_st, k_sh, vcache, v_sb, v_st, v_sh, B, H, D, dtype, 0,
+                              last_pos, cache_cap, window_hint, r, w, eps, y, stream, &c);
+  if (rc == -1) return ok();
+  if (rc != MSA_OK) return rc;
+  const size_t need = msa_decode_workspace_bytes(B, H, D, cache_cap);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(MSA_ERR_WORKSPACE, "decode workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  c.part = (float*)workspace;
+  return hip_status(msa::launch_decode(c), "msa_decode_at launch");
 }
 
 // ---------------------------------------------------------------------------
@@ -382,7 +405,7 @@ int msa_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh, const void* kc
                        const float* w, float eps, void* y, void* stream) {
   msa::DecodeCall c;
   int rc = decode_setup(q, q_sb, q_sh, kcache, k_sb, k_st, k_sh, vcache, v_sb, v_st, v_sh, B, H, D, dtype,
-                        cache_len, cache_cap, window_hint, r, w, eps, y, stream, &c);
+                        cache_len, nullptr, cache_cap, window_hint, r, w, eps, y, stream, &c);
   if (rc == -1) return ok();
   if (rc != MSA_OK) return rc;
   const size_t need = msa_decode_workspace_bytes(B, H, D, cache_len);

@@ -93,6 +93,9 @@ struct DecodeCall {
   const float* r; const float* w; float eps;
   void* y; float* part;
   int blocks;  // grid size of the partial-sum kernel (any value >= 1 gives the same result)
+  int single;  // 1: one block per head walks its chunks (no partials); same result
+  const int64_t* last_pos;  // device position of the newest key, or null (len is the length)
+  int cap;                  // cache capacity (bounds the device length)
   hipStream_t stream;
 };
 int decode_chunk_keys();

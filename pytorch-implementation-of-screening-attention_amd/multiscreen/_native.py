@@ -42,6 +42,8 @@ _SIGS = {
     "msa_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "msa_decode": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                         _i, _i, _i, _i, _i, _i, _i, _p, _p, _f, _p, _p, _sz, _p]),
+    "msa_decode_at": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+                           _i, _i, _i, _i, _p, _i, _i, _p, _p, _f, _p, _p, _sz, _p]),
     "msa_decode_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                                 _i, _i, _i, _i, _i, _i, _i, _p, _p, _f, _p, _p]),
     "msa_timer_arm": (_i, [_i, _i]),

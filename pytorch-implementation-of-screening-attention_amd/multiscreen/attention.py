@@ -160,20 +160,33 @@ class ScreeningAttention(nn.Module):
         y = self.core(q, k, v)
         return self.out_proj(y.reshape(B, T, self.d_model))
 
-    def decode(self, x: torch.Tensor, cache, pos: int) -> torch.Tensor:
-        """x (B,1,d) is the token at position `pos`; returns its attention output (B,1,d)."""
+    def decode(self, x: torch.Tensor, cache, pos, rw=None) -> torch.Tensor:
+        """x (B,1,d) is the token at position `pos`; returns its attention output (B,1,d).
+
+        pos: an int, or (on GPU) a CUDA int64 tensor of one element holding the
+        position, so that the step can be captured once and replayed as the
+        position advances on the device.  rw: optional (r, w) fp32 tensors
+        computed beforehand (exp(s_r)+1, exp(s_v)+1), for callers decoding
+        many tokens with fixed parameters."""
         if not self.causal:
             raise RuntimeError("KV-cache decode is defined for causal self-attention only")
         B = x.shape[0]
         q, k, v = self.project_qkv(x, x, x)
+        r, w = rw if rw is not None else (self.sharpness(), self.window())
+        if torch.is_tensor(pos):
+            if not x.is_cuda:
+                raise RuntimeError("a device position needs the GPU decode path")
+            cache.store_at(k, v, pos)
+            y = ops.decode_step_at(q[:, 0].to(cache.k.dtype), cache.k, cache.v, pos, r, w, self.eps,
+                                   cache.workspace, cache.window_hint).to(x.dtype)
+            return self.out_proj(y.reshape(B, 1, self.d_model))
         cache.store(k, v, pos)
-        kc, vc = cache.k[:, :pos + 1], cache.v[:, :pos + 1]
-        w, r = self.window(), self.sharpness()
         if x.is_cuda:
             # the cache's dtype is the kernel's (fp16 models keep an fp32 cache)
             y = ops.decode_step(q[:, 0].to(cache.k.dtype), cache.k, cache.v, pos + 1, r, w, self.eps,
                                 cache.workspace, cache.window_hint).to(x.dtype)
         else:
+            kc, vc = cache.k[:, :pos + 1], cache.v[:, :pos + 1]
             y = screening_core_dense(q, kc, vc, r, w, True, self.eps, q_offset=pos)[:, 0]
         return self.out_proj(y.reshape(B, 1, self.d_model))
 
@@ -208,3 +221,9 @@ class KVCache:
             raise IndexError(f"KV cache capacity {self.k.shape[1]} exceeded at position {pos + T}")
         self.k[:, pos:pos + T] = k.to(self.k.dtype)
         self.v[:, pos:pos + T] = v.to(self.v.dtype)
+
+    def store_at(self, k, v, pos):
+        """k, v (B,1,H,D) at the position held by the device int64 tensor pos
+        (one element).  The caller keeps pos below the capacity."""
+        self._k.index_copy_(2, pos, k.permute(0, 2, 1, 3).to(self._k.dtype))
+        self._v.index_copy_(2, pos, v.permute(0, 2, 1, 3).to(self._v.dtype))

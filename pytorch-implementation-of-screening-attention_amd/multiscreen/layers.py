@@ -51,10 +51,10 @@ class MultiscreenBlock(nn.Module):
         x = x + self.attn.prefill(normed, cache)
         return x + self.ffn(self.norm2(x))
 
-    def decode(self, x: torch.Tensor, cache, pos: int) -> torch.Tensor:
-        """One token x (B,1,d) at position `pos`, attending to the cache."""
+    def decode(self, x: torch.Tensor, cache, pos, rw=None) -> torch.Tensor:
+        """One token x (B,1,d) at position `pos` (int or device tensor), attending to the cache."""
         normed = self.norm1(x)
-        x = x + self.attn.decode(normed, cache, pos)
+        x = x + self.attn.decode(normed, cache, pos, rw)
         return x + self.ffn(self.norm2(x))
 
 

@@ -171,6 +171,32 @@ def screening_core(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, 
     return ScreeningCoreFunction.apply(q, k, v, r, w, causal, eps, key_padding_mask, dropout_p, seed)
 
 
+def _decode_args(q, kcache, vcache, r, w):
+    if not q.is_cuda:
+        raise RuntimeError("decode_step runs on the GPU only (got a CPU tensor)")
+    if q.dtype not in _DTYPES or kcache.dtype != q.dtype or vcache.dtype != q.dtype:
+        raise TypeError(f"decode_step needs q and the caches in one of float32 / bfloat16, got "
+                        f"{q.dtype}, {kcache.dtype}, {vcache.dtype}")
+    B, H, D = q.shape
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    es = q.element_size()
+    kcache, vcache = _as_bthd(kcache, "kcache", es), _as_bthd(vcache, "vcache", es)
+    if kcache.shape != vcache.shape or kcache.shape[0] != B or kcache.shape[2:] != (H, D):
+        raise ValueError(f"cache shapes {tuple(kcache.shape)}/{tuple(vcache.shape)} do not match q {tuple(q.shape)}")
+    dev = q.device
+    r32 = r.detach().to(device=dev, dtype=torch.float32).contiguous()
+    w32 = w.detach().to(device=dev, dtype=torch.float32).contiguous()
+    return q, kcache, vcache, r32, w32
+
+
+def _decode_workspace(L, workspace, B, H, D, length, dev):
+    need = int(L.msa_decode_workspace_bytes(B, H, D, int(length)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty((max(need, 16),), dtype=torch.uint8, device=dev)
+    return workspace
+
+
 def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None, window_hint=0):
     """Screening attention of one new query per (b, h) against a KV cache.
 
@@ -180,32 +206,43 @@ def decode_step(q, kcache, vcache, cache_len, r, w, eps=1e-8, workspace=None, wi
     Returns y (B, H, D) = TanhNorm(h) of that token.
     """
     L = _native.lib()
-    if not q.is_cuda:
-        raise RuntimeError("decode_step runs on the GPU only (got a CPU tensor)")
-    if q.dtype not in _DTYPES or kcache.dtype != q.dtype or vcache.dtype != q.dtype:
-        raise TypeError(f"decode_step needs q and the caches in one of float32 / bfloat16, got "
-                        f"{q.dtype}, {kcache.dtype}, {vcache.dtype}")
-    dt = _DTYPES[q.dtype]
+    q, kcache, vcache, r32, w32 = _decode_args(q, kcache, vcache, r, w)
     B, H, D = q.shape
-    if q.stride(2) != 1:
-        q = q.contiguous()
-    es = q.element_size()
-    kcache, vcache = _as_bthd(kcache, "kcache", es), _as_bthd(vcache, "vcache", es)
     dev = q.device
     y = torch.empty((B, H, D), dtype=q.dtype, device=dev)
-    need = int(L.msa_decode_workspace_bytes(B, H, D, int(cache_len)))
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
-        workspace = torch.empty((max(need, 16),), dtype=torch.uint8, device=dev)
-    r32 = r.detach().to(device=dev, dtype=torch.float32).contiguous()
-    w32 = w.detach().to(device=dev, dtype=torch.float32).contiguous()
-    if kcache.shape != vcache.shape or kcache.shape[0] != B or kcache.shape[2:] != (H, D):
-        raise ValueError(f"cache shapes {tuple(kcache.shape)}/{tuple(vcache.shape)} do not match q {tuple(q.shape)}")
+    workspace = _decode_workspace(L, workspace, B, H, D, cache_len, dev)
     rc = L.msa_decode(q.data_ptr(), q.stride(0), q.stride(1),
                       *_args_bthd(kcache), *_args_bthd(vcache),
-                      B, H, D, dt, int(cache_len), int(kcache.shape[1]), int(window_hint),
+                      B, H, D, _DTYPES[q.dtype], int(cache_len), int(kcache.shape[1]), int(window_hint),
                       r32.data_ptr(), w32.data_ptr(),
                       float(eps),
                       y.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
                       _stream_ptr(dev))
     _native.check(rc, "msa_decode")
+    return y
+
+
+def decode_step_at(q, kcache, vcache, last_pos, r, w, eps=1e-8, workspace=None, window_hint=0):
+    """decode_step with the query's position in device memory: last_pos is a
+    CUDA int64 tensor of one element, the position of the newest key, so the
+    cache holds positions [0, last_pos] (the length is clamped to the
+    capacity).  Launches depend only on the shapes, so a captured call stays
+    valid as last_pos advances on the device."""
+    L = _native.lib()
+    q, kcache, vcache, r32, w32 = _decode_args(q, kcache, vcache, r, w)
+    if not (last_pos.is_cuda and last_pos.dtype == torch.int64 and last_pos.numel() == 1):
+        raise TypeError("last_pos must be a CUDA int64 tensor of one element")
+    B, H, D = q.shape
+    dev = q.device
+    cap = int(kcache.shape[1])
+    y = torch.empty((B, H, D), dtype=q.dtype, device=dev)
+    workspace = _decode_workspace(L, workspace, B, H, D, cap, dev)
+    rc = L.msa_decode_at(q.data_ptr(), q.stride(0), q.stride(1),
+                         *_args_bthd(kcache), *_args_bthd(vcache),
+                         B, H, D, _DTYPES[q.dtype], last_pos.data_ptr(), cap, int(window_hint),
+                         r32.data_ptr(), w32.data_ptr(),
+                         float(eps),
+                         y.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                         _stream_ptr(dev))
+    _native.check(rc, "msa_decode_at")
     return y
