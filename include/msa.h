@@ -78,7 +78,9 @@ const char* msa_last_error(void);
 
 /* Bytes of forward workspace: scratch for one unit-normalised copy of K (key
  * padding applied, rows padded to a multiple of 64, head_dim padded to
- * 32/64/128) that the forward stages through LDS.  Not needed afterwards. */
+ * 32/64/128) that the forward stages through LDS, and the screen's work plan.
+ * Enough for a causal or a non-causal call of this shape.  Not needed
+ * afterwards. */
 size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
 /* Number of uint32 words of the live-unit bitmap: one bit per

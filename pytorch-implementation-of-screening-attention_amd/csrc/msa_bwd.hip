@@ -202,8 +202,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
     ku_hi = jhi >= jlo ? (int)(jhi / kUnit) : ku_lo - 1;
   }
   const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + qu) * a.nku_words;
-  auto bitf = [brow](int u) { return ((brow[u >> 5] >> (u & 31)) & 1u) != 0u; };
-  BitWalk<decltype(bitf)> walk(bitf, ku_lo, ku_hi);
+  RowWalk walk(brow, ku_lo, ku_hi);
   int cur = walk.next();
   const int64_t nbh = (int64_t)a.B * a.H;
   const int nqu = 2 * a.nqt;
@@ -473,9 +472,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     qu_hi = ihi >= ilo && k0 < a.Tk ? (int)(ihi / kUnit) : qu_lo - 1;
   }
   const uint32_t* bcol = a.bits + (int64_t)bh * 2 * a.nqt * a.nku_words + (ku >> 5);
-  const int nw = a.nku_words, sh = ku & 31;
-  auto bitf = [bcol, nw, sh](int qu) { return ((bcol[(int64_t)qu * nw] >> sh) & 1u) != 0u; };
-  BitWalk<decltype(bitf)> walk(bitf, qu_lo, qu_hi);
+  ColWalk walk(bcol, a.nku_words, ku & 31, qu_lo, qu_hi);
   int cur = walk.next();
   if (cur < 0) {  // wave-uniform: no live query unit, dk = dv = 0
     if (jvalid)

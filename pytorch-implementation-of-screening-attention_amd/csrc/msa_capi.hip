@@ -168,9 +168,16 @@ int msa_version(void) { return (0 << 16) | (1 << 8) | 0; }
 const char* msa_last_error(void) { return g_last_error.c_str(); }
 
 size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype) {
-  msa::Geometry g;
-  if (check_geometry(B, H, Tq, Tk, D, dtype, 1, &g) != MSA_OK) return 0;
-  return msa::fwd_ws_bytes(g);
+  // the screen plan's size depends on the mask (a non-causal window reaches
+  // both ways, so more items): the larger of the two serves either call
+  size_t need = 0;
+  for (int causal = 0; causal <= 1; ++causal) {
+    msa::Geometry g;
+    if (check_geometry(B, H, Tq, Tk, D, dtype, causal, &g) != MSA_OK) return 0;
+    const size_t n = msa::fwd_ws_bytes(g);
+    need = n > need ? n : need;
+  }
+  return need;
 }
 
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk) {

@@ -564,29 +564,79 @@ struct StageTile {
 template <typename T, int DP>
 using WaveStage = StageTile<T, DP, 32, 64>;
 
-// Set bits of a sequence of bitmap positions lo..hi, visited in increasing
-// order 64 at a time through a wave ballot; bit(p) reads position p.  All
-// state is wave-uniform.
-template <typename F>
-struct BitWalk {
-  F bit;
-  int base, hi;
-  unsigned long long mask;
-  __device__ BitWalk(F f, int lo, int hi_) : bit(f), base(lo), hi(hi_) {
-    const int p = base + (int)(threadIdx.x & 63);
-    mask = __ballot(p <= hi && bit(p));
+// Set bits lo..hi of one bitmap row (position u = bit u%32 of word u/32),
+// visited in increasing order.  Lane l holds word w0 + l, so one load round
+// trip brings 2048 positions: a row's walk waits on memory once, not once
+// per 64 positions.  The words at the range's ends are masked to it.
+struct RowWalk {
+  const uint32_t* row;
+  uint32_t word;  // this lane's word of the current 64-word window
+  int w0, lo, hi;
+  __device__ RowWalk(const uint32_t* r, int lo_, int hi_) : row(r), w0(lo_ >> 5), lo(lo_), hi(hi_) { fill(); }
+  __device__ inline void fill() {
+    const int wi = w0 + (int)(threadIdx.x & 63);
+    uint32_t x = lo <= hi && wi <= (hi >> 5) ? row[wi] : 0u;
+    if (wi == (lo >> 5)) x &= ~0u << (lo & 31);
+    if (wi == (hi >> 5)) x &= ~0u >> (31 - (hi & 31));
+    word = x;
   }
   // next set position, or -1
   __device__ inline int next() {
-    while (mask == 0ull) {
-      base += 64;
-      if (base > hi) return -1;
-      const int p = base + (int)(threadIdx.x & 63);
-      mask = __ballot(p <= hi && bit(p));
+    for (;;) {
+      const unsigned long long m = __ballot(word != 0u);
+      if (m != 0ull) {
+        const int L = (int)__builtin_ctzll(m);
+        const uint32_t wv = (uint32_t)__builtin_amdgcn_readlane((int)word, L);
+        if ((int)(threadIdx.x & 63) == L) word &= word - 1u;
+        return 32 * (w0 + L) + (int)__builtin_ctz(wv);
+      }
+      w0 += 64;
+      if (lo > hi || w0 > (hi >> 5)) return -1;
+      fill();
     }
-    const int idx = base + __builtin_ctzll(mask);
-    mask &= mask - 1ull;
-    return idx;
+  }
+};
+
+// Set bits of one bitmap column: rows lo..hi of bit `sh` in the words
+// col[row * stride], visited in increasing order.  One fill issues the loads
+// of 256 rows (four per lane) before the first ballot waits, so a column of
+// up to 256 rows costs one load round trip.  All state is wave-uniform.
+struct ColWalk {
+  const uint32_t* col;
+  int stride, sh, base, end, hi;
+  unsigned long long m0, m1, m2, m3;  // rows base .. base+255, 64 per mask
+  __device__ ColWalk(const uint32_t* c, int stride_, int sh_, int lo, int hi_)
+      : col(c), stride(stride_), sh(sh_), base(lo), hi(hi_) { fill(); }
+  __device__ inline uint32_t word(int p) const { return p <= hi ? col[(int64_t)p * stride] : 0u; }
+  __device__ inline void fill() {
+    const int p = base + (int)(threadIdx.x & 63);
+    const uint32_t x0 = word(p), x1 = word(p + 64), x2 = word(p + 128), x3 = word(p + 192);
+    m0 = __ballot(((x0 >> sh) & 1u) != 0u);
+    m1 = __ballot(((x1 >> sh) & 1u) != 0u);
+    m2 = __ballot(((x2 >> sh) & 1u) != 0u);
+    m3 = __ballot(((x3 >> sh) & 1u) != 0u);
+    end = base + 256;
+  }
+  // next set position, or -1
+  __device__ inline int next() {
+    for (;;) {
+      if (m0 != 0ull) {
+        const int idx = base + (int)__builtin_ctzll(m0);
+        m0 &= m0 - 1ull;
+        return idx;
+      }
+      if ((m1 | m2 | m3) != 0ull) {
+        m0 = m1;
+        m1 = m2;
+        m2 = m3;
+        m3 = 0ull;
+        base += 64;
+        continue;
+      }
+      base = end;
+      if (base > hi) return -1;
+      fill();
+    }
   }
 };
 
@@ -622,7 +672,7 @@ __device__ inline void xcd_interleave(int& bx, int& by) {
 // keyed as +inf, so the ranks 0..H-1 are a permutation of the heads whatever
 // the windows hold (NaN, infinities, duplicates): every (b, h) gets exactly
 // one block row.  The mapping also returns the selected head's r_h and w_h:
-// lane o loads r[o] and w[o] in the one round trip the ranking needs, and the
+// lane o receives r[o] and w[o] from the loads the ranking needs, and the
 // head's values come back by readlane (no second dependent load).
 __device__ inline float window_rank_key(float w) { return w != w ? INFINITY : w; }
 __device__ inline void xcd_interleave_ranked(const float* r, const float* w, int H, int& bx, int& by, float& rh,
@@ -635,7 +685,16 @@ __device__ inline void xcd_interleave_ranked(const float* r, const float* w, int
     return;
   }
   const int lane = threadIdx.x & 63;
-  const float wraw = lane < H ? w[lane] : 0.0f, rraw = lane < H ? r[lane] : 0.0f;
+  // r and w through uniform (scalar-cache) loads: every wave reads the same
+  // few words, and the scalar path does not queue behind the vector loads of
+  // the other waves on the CU
+  float wraw = 0.0f, rraw = 0.0f;
+#pragma unroll 8
+  for (int o = 0; o < H; ++o) {
+    const float wo = w[o], ro = r[o];
+    wraw = lane == o ? wo : wraw;
+    rraw = lane == o ? ro : rraw;
+  }
   const float wl = window_rank_key(wraw);  // lane o holds head o's key
   const int B = BH / H, rk = by / B, b = by % B;
   int rank = 0;

@@ -702,8 +702,7 @@ void fwd_live_kernel(FwdKArgs a) {
     key_range<kUnit>(a, hp, causal, qa, qb, ku_lo, ku_hi);
   }
   const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + qu) * a.nku_words;
-  auto bitf = [brow](int u) { return ((brow[u >> 5] >> (u & 31)) & 1u) != 0u; };
-  BitWalk<decltype(bitf)> walk(bitf, ku_lo, ku_hi);
+  RowWalk walk(brow, ku_lo, ku_hi);
   int cur = walk.next();
   if (cur < 0) {  // wave-uniform: no live key unit, y = 0 and |h| = 0
     if (valid) {

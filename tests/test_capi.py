@@ -34,10 +34,12 @@ def test_version_and_sizes():
     L = _native.lib()
     assert L.msa_version() == (0 << 16) | (1 << 8)
     # B=4, T=8192, H=8, D=64 bf16: one normalised K^ copy, then the screen's
-    # work-plan table: 32 lanes x kmax entries of 32 bytes (kmax = 68 here:
-    # 4 heads per XCD x 68 items of at most 40 steps, over 4 lanes)
+    # work-plan table: 32 lanes x kmax entries of 32 bytes.  The size serves a
+    # causal or a non-causal call: kmax = 68 causal (4 heads per XCD x 68
+    # items of at most 40 steps, over 4 lanes), 128 non-causal (every group's
+    # offsets span 131 tiles: 4 items a group), so 128
     one = 4 * 8 * 8192 * 64 * 2
-    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == one + 32 * 68 * 32
+    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == one + 32 * 128 * 32
     # 2*nqt query-unit rows of ceil(2*nkt/32) words per (b, h)
     assert L.msa_tile_bits_words(4, 8, 8192, 8192) == 4 * 8 * 256 * 8
     assert L.msa_tile_bits_words(1, 1, 65, 65) == 4

@@ -73,3 +73,41 @@ def test_cfg2_full_shape_forward_backward(variant):
     clear = a > 1e-2
     marked = units[P["b"], P["h"], P["i"] // 32, P["j"] // 32]
     assert np.all(marked[clear])
+
+
+# Key units whose bitmap column spans more than 256 query units (windows wider
+# than 8192 keys, causal; or wider than 4096 keys both ways, non-causal): the
+# dK/dV pass walks such a column in more than one 256-row load.  Every output
+# compared in full with the live-pair float64 oracle.
+@pytest.mark.parametrize("causal,T,w", [(True, 16384, [12000.0, 16384.0]), (False, 16384, [5000.0, 700.0])],
+                         ids=["causal_T16384", "noncausal_T16384"])
+def test_long_bitmap_columns_forward_backward(causal, T, w):
+    from multiscreen import ops
+    B, H, D = 1, 2, 64
+    g = torch.Generator().manual_seed(11)
+    q, k, v, dy = (torch.randn(B, T, H, D, generator=g).bfloat16() for _ in range(4))
+    r = [1.3, 1.6]
+    _say(f"long columns: causal={causal} T={T} w={w}")
+    dev = "cuda"
+    rg, wg = torch.tensor(r, device=dev), torch.tensor(w, device=dev)
+    qd, kd, vd, dyd = (t.to(dev) for t in (q, k, v, dy))
+    y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None)
+    dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dyd)
+    torch.cuda.synchronize()
+    got = {n: np64(t) for n, t in zip(("y", "dq", "dk", "dv", "dr", "dw"), (y, dq, dk, dv, dr, dw))}
+    units = _unit_bits(bits, B, H, T)
+    # some live key unit's column reaches past the first 256 query units of its range
+    kus = np.nonzero(units.any(axis=2))
+    span = 0
+    for b_, h_, ku in zip(*kus):
+        qus = np.nonzero(units[b_, h_, :, ku])[0]
+        lo = ku if causal else max(0, ku - int(np.ceil(w[h_] / 32)))
+        span = max(span, int(qus.max()) - lo)
+    assert span >= 256, span
+    yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), np.array(r), np.array(w), np64(dy), causal)
+    _say(f"long columns: {len(P['i'])} live pairs, widest column reach {span} units")
+    for name, want in zip(("y", "dq", "dk", "dv", "dr", "dw"), (yref,) + tuple(gref)):
+        assert np.max(np.abs(want)) > 0, f"{name} vacuous"
+        e = rel_err(got[name], want)
+        _say(f"long columns: {name} rel err {e:.3e}")
+        assert e <= TOL, f"{name}: rel err {e:.3e} > {TOL}"
