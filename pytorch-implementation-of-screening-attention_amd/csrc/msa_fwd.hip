@@ -76,12 +76,15 @@ struct PrepKArgs {
 // Per-XCD mode: the heads of XCD x.  Heads are ranked widest window first
 // (NaN keyed as widest, ties by index: a permutation); rank k goes to XCD
 // (k/8 odd ? 7 - k%8 : k%8) as its (k/8)-th head.  Above kPlanMaxRanked heads
-// the ranking is skipped: slot jh of XCD x is head 8*jh + x.
+// the ranking is skipped: slot jh of XCD x is head 8*jh + x.  The count
+// follows the same rule as the assignment in each mode, so every slot below
+// it holds a head and every head has a slot.
 constexpr int kPlanMaxRanked = 512;
 constexpr int kPlanMaxHeads = 512;  // head slots a planner block keeps in LDS
 __device__ inline int xcd_head_count(int BH, int x) {
+  const bool ranked = BH <= kPlanMaxRanked;
   int nh = 0;
-  for (int jh = 0; 8 * jh < BH; ++jh) nh += 8 * jh + ((jh & 1) ? 7 - x : x) < BH ? 1 : 0;
+  for (int jh = 0; 8 * jh < BH; ++jh) nh += 8 * jh + (ranked && (jh & 1) ? 7 - x : x) < BH ? 1 : 0;
   return nh;
 }
 // keys[h] (the window ranking key of head h) are in LDS when B*H <= kPlanMaxRanked.
