@@ -36,6 +36,7 @@ sys.path.insert(0, os.path.join(HERE, "pytorch-implementation-of-screening-atten
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 TILE_FLOP = 2 * 64 * 64 * 64  # one 64x64 tile product with D=64
+TIMER_EVERY = 10              # timed-region launches of the dominant kernel: one in 10 carries events
 KERNELS = {1: "prep_k_kernel", 2: "fwd_screen_kernel", 3: "fwd_live_kernel", 4: "dkdv_kernel",
            5: "dq_kernel"}   # msa_kernel_id values (include/msa.h)
 
@@ -43,8 +44,10 @@ KERNELS = {1: "prep_k_kernel", 2: "fwd_screen_kernel", 3: "fwd_live_kernel", 4: 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    # the GPU reaches its steady clocks after about 50 ms of back-to-back
+    # steps (the first steps run up to 8% slower): 300 warmup steps are about 60 ms
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=300)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-configs", action="store_true", help="skip the configs[2..4] legs")
@@ -396,9 +399,12 @@ def main():
     dom_id = {name: kid for kid, name in KERNELS.items()}[dom]
 
     # timed region: exactly `steps` steps, synchronised on both sides; the
-    # dominant kernel's launches are bracketed by HIP events on its stream
+    # dominant kernel's launches in one step of TIMER_EVERY are bracketed by HIP
+    # events on its stream (each event pair adds a few microseconds of stream
+    # time, so they are not put on every step)
     import ctypes
-    assert L.msa_timer_arm(dom_id, args.steps) == 0
+    n_timed = (args.steps + TIMER_EVERY - 1) // TIMER_EVERY
+    assert L.msa_timer_arm_every(dom_id, n_timed, TIMER_EVERY) == 0
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -410,8 +416,8 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_step = t0.elapsed_time(t1) / args.steps
-    buf = (ctypes.c_float * args.steps)()
-    n = L.msa_timer_read(dom_id, buf, args.steps)
+    buf = (ctypes.c_float * n_timed)()
+    n = L.msa_timer_read(dom_id, buf, n_timed)
     L.msa_timer_arm(0, 0)
     dom_ms = sum(buf[i] for i in range(n)) / max(1, n)
 
@@ -446,6 +452,7 @@ def main():
                    "global_batch": B, "seq_len": T, "heads": H, "head_dim": D,
                    "r": [round(x, 4) for x in r], "w": [round(x, 1) for x in w]},
         "roofline": {"bound": "mfma", "kernel": dom, "kernel_ms": round(dom_ms, 4),
+                     "kernel_ms_launches": n, "kernel_ms_every": TIMER_EVERY,
                      "achieved": round(achieved, 2) if achieved else None,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 5) if achieved else None,

@@ -212,12 +212,17 @@ int msa_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
  * msa_timer_read(kernel, ...) waits for that kernel's recorded pairs and
  * writes their durations in milliseconds, returning how many were recorded
  * (-1 on error).  msa_timer_arm(0, 0) disarms every kernel.  Process-wide; not
- * for concurrent use from several threads. */
+ * for concurrent use from several threads.
+ * msa_timer_arm_every(kernel, n, every) records launches 0, every, 2*every, ...
+ * of that kernel (n pairs): a timed loop then carries the event markers on
+ * one launch in `every` only (each recorded pair adds a few microseconds of
+ * stream time).  Measurement helpers: no counterpart in the reference. */
 enum msa_kernel_id {
   MSA_K_PREP_K = 1, MSA_K_FWD_SCREEN = 2, MSA_K_FWD_LIVE = 3, MSA_K_DKDV = 4,
   MSA_K_DQ = 5, /* 6: unused (no separate dr/dw reduction launch) */ MSA_K_DECODE = 7
 };
 int msa_timer_arm(int kernel, int n);
+int msa_timer_arm_every(int kernel, int n, int every);
 int msa_timer_read(int kernel, float* ms, int n);
 
 /* Device self-test of the MFMA operand layouts the kernels assume: writes the

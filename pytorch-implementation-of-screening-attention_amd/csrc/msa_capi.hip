@@ -84,7 +84,9 @@ int hip_status(hipError_t e, const char* what) {
 
 // One armed event list per kernel id; several kernels may be armed at once.
 struct TimerSlot {
-  int next = 0;
+  int next = 0;     // recorded pairs
+  int every = 1;    // record launches 0, every, 2*every, ...
+  int launch = 0;   // launches seen since arming
   std::vector<hipEvent_t> start, stop;
 };
 struct TimerState {
@@ -102,6 +104,8 @@ void timer_clear(TimerSlot& s) {
   s.start.clear();
   s.stop.clear();
   s.next = 0;
+  s.every = 1;
+  s.launch = 0;
 }
 
 }  // namespace
@@ -111,19 +115,20 @@ void timer_begin(int kernel, hipStream_t s) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
   TimerSlot& sl = t.slot[kernel];
-  if (sl.next < (int)sl.start.size()) (void)hipEventRecord(sl.start[sl.next], s);
+  if (sl.next < (int)sl.start.size() && sl.launch % sl.every == 0) (void)hipEventRecord(sl.start[sl.next], s);
 }
 void timer_end(int kernel, hipStream_t s) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
   TimerSlot& sl = t.slot[kernel];
-  if (sl.next < (int)sl.stop.size()) (void)hipEventRecord(sl.stop[sl.next++], s);
+  if (sl.next < (int)sl.stop.size() && sl.launch % sl.every == 0) (void)hipEventRecord(sl.stop[sl.next++], s);
+  ++sl.launch;
 }
 }  // namespace msa
 
 extern "C" {
 
-int msa_timer_arm(int kernel, int n) {
+int msa_timer_arm_every(int kernel, int n, int every) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> g(t.mu);
   if (kernel == 0) {
@@ -131,8 +136,10 @@ int msa_timer_arm(int kernel, int n) {
     return ok();
   }
   if (kernel < MSA_K_PREP_K || kernel > MSA_K_DECODE) return fail(MSA_ERR_INVALID, "unknown kernel id %d", kernel);
+  if (every < 1) return fail(MSA_ERR_INVALID, "every must be >= 1 (got %d)", every);
   TimerSlot& sl = t.slot[kernel];
   timer_clear(sl);
+  sl.every = every;
   for (int i = 0; i < n; ++i) {
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess) return fail(MSA_ERR_HIP, "hipEventCreate failed");
@@ -145,6 +152,8 @@ int msa_timer_arm(int kernel, int n) {
   }
   return ok();
 }
+
+int msa_timer_arm(int kernel, int n) { return msa_timer_arm_every(kernel, n, 1); }
 
 int msa_timer_read(int kernel, float* ms, int n) {
   TimerState& t = timer();

@@ -47,6 +47,7 @@ _SIGS = {
     "msa_decode_noalloc": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                                 _i, _i, _i, _i, _i, _i, _i, _p, _p, _f, _p, _p]),
     "msa_timer_arm": (_i, [_i, _i]),
+    "msa_timer_arm_every": (_i, [_i, _i, _i]),
     "msa_timer_read": (_i, [_i, ctypes.POINTER(ctypes.c_float), _i]),
     "msa_selftest_mfma": (_i, [_p, _p, _p, _p, _p, _p, _p]),
 }
