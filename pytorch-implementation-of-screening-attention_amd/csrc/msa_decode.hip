@@ -30,7 +30,7 @@
 namespace msa {
 
 constexpr int kChunk = 2048;
-constexpr int kDecUnroll = 8;
+constexpr int kDecUnroll = 16;  // K row loads per lane in flight per round
 
 struct DecArgs {
   const void* q; int64_t q_sb, q_sh;
