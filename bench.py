@@ -20,6 +20,13 @@ Also reported:
                        algorithmic flop C(|W|+|A|) and bf16-peak fraction
   cfg5_decode_literal  configs[4] as written: ms per generated token, eager
                        and replayed from a captured HIP graph (same tokens)
+  cfg2_trained_regime  the configs[1] shape with inputs in the regime its
+                       text describes (~5% of in-window alpha non-zero)
+  cfg2_f16             the headline workload in float16
+  ref_fused_module_fwd the reference's own published fused benchmark
+                       (module forward, fp32, T = 512..4096) with peak memory
+  peak_memory_mb       device memory of one headline step
+The supplementary legs run before the headline's warm-up and timed steps.
 Prints ONE JSON line.
 """
 
@@ -68,6 +75,32 @@ def cfg2_inputs(seed=0):
     r = (1.9 + 0.2 * torch.rand(H, generator=g)).tolist()
     w = (256.0 + (8192.0 - 256.0) * torch.rand(H, generator=g)).tolist()
     q, k, v, dy = (torch.randn(B, T, H, D, generator=g).bfloat16() for _ in range(4))
+    return q, k, v, dy, r, w
+
+
+def trained_regime_inputs(seed=0, n_clusters=18, rho=0.8, B=4, T=8192):
+    """The configs[1] shape, r and w with inputs in the regime its text
+    describes ("~95% of alpha at zero", the trained-model figure of the
+    reference's README.md:33), which i.i.d. N(0,1) inputs do not reach
+    (99.99% zero there).  Each (b, t, h) draws one of n_clusters per-head
+    centres c; q = rho c + sqrt(1 - rho^2) n_q and k likewise (own noise),
+    v, dO ~ N(0,1).  Same-cluster pairs have s near rho^2 = 0.64, above every
+    head's threshold 1 - 1/r in [0.47, 0.53] for most pairs, and other pairs
+    rarely pass, so about 0.9/18 = 5% of in-window pairs are live and nearly
+    every in-window 32x32 unit holds one."""
+    import torch
+    H, D = 8, 64
+    g = torch.Generator().manual_seed(seed)   # r and w as cfg2_inputs draws them
+    r = (1.9 + 0.2 * torch.rand(H, generator=g)).tolist()
+    w = (256.0 + (8192.0 - 256.0) * torch.rand(H, generator=g)).tolist()
+    g = torch.Generator().manual_seed(seed + 1000)
+    centres = torch.randn(H, n_clusters, D, generator=g)
+    assign = torch.randint(0, n_clusters, (B, T, H), generator=g)
+    base = centres[torch.arange(H).view(1, 1, H), assign]
+    sig = math.sqrt(1.0 - rho * rho)
+    q = (rho * base + sig * torch.randn(B, T, H, D, generator=g)).bfloat16()
+    k = (rho * base + sig * torch.randn(B, T, H, D, generator=g)).bfloat16()
+    v, dy = (torch.randn(B, T, H, D, generator=g).bfloat16() for _ in range(2))
     return q, k, v, dy, r, w
 
 
@@ -363,6 +396,144 @@ def cfg5_bench(torch, new_tokens=256):
                     "ms_per_token_graph: the same steps replayed from one captured HIP graph"}
 
 
+def live_pair_fraction(q, k, r, w, torch, rows=256, seed=0):
+    """Fraction of in-window causal pairs with alpha > 0, on `rows` sampled
+    queries per (b, h) of batch row 0 (every key of their windows), in fp32
+    from the rounded inputs."""
+    B, T, H, D = q.shape
+    g = torch.Generator(device=q.device).manual_seed(seed)
+    live = tot = 0
+    for h in range(H):
+        wc = int(math.ceil(w[h]))
+        idx = torch.randint(0, T, (rows,), device=q.device, generator=g)
+        qn = torch.nn.functional.normalize(q[0, idx, h].float(), dim=-1)
+        kn = torch.nn.functional.normalize(k[0, :, h].float(), dim=-1)
+        s = qn @ kn.T                                             # (rows, T)
+        d = idx.view(-1, 1) - torch.arange(T, device=q.device).view(1, -1)
+        inside = (d >= 0) & (d < wc)
+        live += int(((s > 1.0 - 1.0 / r[h]) & inside).sum())
+        tot += int(inside.sum())
+    return live / max(tot, 1)
+
+
+def step_legs(L, ops, torch, q, k, v, dy, r, w, reps=10):
+    """fwd+bwd step time (events, after 3 untimed steps), per-kernel event
+    times, tile counts and algorithmic rates of one cfg2-shaped workload."""
+    dev = q.device
+    rg, wg = torch.tensor(r, device=dev), torch.tensor(w, device=dev)
+    B, T, H, D = q.shape
+
+    def step():
+        y, hnorm, bits = ops.fwd_raw(q, k, v, rg, wg, True, 1e-8, None)
+        ops.bwd_raw(q, k, v, rg, wg, True, 1e-8, y, hnorm, bits, dy)
+        return bits
+    for _ in range(3):
+        bits = step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        bits = step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    per_kernel = {name: round(kernel_times(L, kid, step, 3)[0], 4) for kid, name in KERNELS.items()}
+    nW = window_tiles(T, w) * B
+    nU, nA = live_counts(bits, B, H, T)
+    f_total = TILE_FLOP * (nW + 6 * nA)
+    unit_flop = {"fwd_live_kernel": TILE_FLOP * nA, "dq_kernel": TILE_FLOP * nA, "dkdv_kernel": 4 * TILE_FLOP * nA}
+    return {"ms_per_step": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "kernel_ms_event": per_kernel,
+            "tiles": {"window": nW, "active": nA, "active_units_32": nU,
+                      "active_frac_of_window": round(nA / max(nW, 1), 4)},
+            "flop_alg": f_total, "tflops_alg": round(f_total / (ms * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(f_total / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 5),
+            "unit_kernels_frac_bf16_peak": {
+                k_: round(f / (per_kernel[k_] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 5)
+                for k_, f in unit_flop.items()}}
+
+
+def trained_regime_bench(L, ops, torch):
+    """configs[1] shape, r, w and dtype with the trained-regime inputs of
+    trained_regime_inputs (about 5% of in-window alpha non-zero)."""
+    q, k, v, dy, r, w = (t.cuda() if hasattr(t, "cuda") else t for t in trained_regime_inputs(0))
+    out = {"workload": "configs[1] shape (B=4 T=8192 H=8 D=64 bf16 causal, its r and w) with clustered q/k "
+                       "(18 centres per head, rho 0.8): the regime configs[1] describes, ~5% of in-window "
+                       "alpha non-zero",
+           "live_pair_frac_of_window": round(live_pair_fraction(q, k, r, w, torch), 4)}
+    out.update(step_legs(L, ops, torch, q, k, v, dy, r, w))
+    return out
+
+
+def fp16_bench(L, ops, torch, q, k, v, dy, r, w):
+    """The headline workload with the same inputs in float16 (torch.autocast's
+    CUDA dtype, the reference's fused dtype, screening_fwd.py:235)."""
+    out = {"workload": "configs[1] inputs cast to float16 (v_mfma_f32_32x32x16_f16)"}
+    out.update(step_legs(L, ops, torch, *(t.half() for t in (q, k, v, dy)), r, w))
+    return out
+
+
+# The reference's published fused-path numbers (BENCHMARK_REPORT_TRITON.md:61-85,
+# RTX 4060 Ti, triton-windows): module forward latency (final column) and peak
+# memory, forward only (eval) and forward + backward (training).
+REF_TRITON_FWD_MS = {512: 0.681, 1024: 1.389, 2048: 2.825, 4096: 5.858}
+REF_TRITON_FWD_MB = {512: 52.6, 1024: 88.2, 2048: 159.5, 4096: 302.1}
+REF_TRITON_FWDBWD_MB = {512: 98.2, 1024: 168.8, 2048: 303.8}
+
+
+def ref_module_bench(torch, reps=20):
+    """The reference's own fused-path benchmark (benchmarks/bench_triton.py:19-60):
+    ScreeningAttention(512, 8 heads, causal) forward of the whole module in
+    fp32 on x ~ N(0,1) of shape (4, T, 512), s_r = -2 (r = 1.135), default
+    windows; latency (median of `reps` event-timed calls after warm-up) and
+    torch.cuda.max_memory_allocated for the forward (eval, no_grad) and for
+    forward + backward (train)."""
+    from multiscreen import ScreeningAttention
+    torch.manual_seed(0)
+    m = ScreeningAttention(512, num_heads=8, causal=True).cuda()
+    with torch.no_grad():
+        m.s_r.fill_(-2.0)
+    rows = []
+    for T in (512, 1024, 2048, 4096):
+        x = torch.randn(4, T, 512, device="cuda")
+        m.eval()
+        with torch.no_grad():
+            for _ in range(3):
+                m(x, x, x)
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(reps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                m(x, x, x)
+                b.record()
+                torch.cuda.synchronize()
+                times.append(a.elapsed_time(b))
+            torch.cuda.reset_peak_memory_stats()
+            m(x, x, x)
+            torch.cuda.synchronize()
+            mem_fwd = torch.cuda.max_memory_allocated() / 1e6
+        m.train()
+        xg = x.clone().requires_grad_()
+        torch.cuda.reset_peak_memory_stats()
+        m(xg, xg, xg).sum().backward()
+        torch.cuda.synchronize()
+        mem_fb = torch.cuda.max_memory_allocated() / 1e6
+        m.zero_grad(set_to_none=True)
+        ms = sorted(times)[len(times) // 2]
+        row = {"T": T, "fwd_ms": round(ms, 4), "fwd_peak_mb": round(mem_fwd, 1), "fwd_bwd_peak_mb": round(mem_fb, 1),
+               "ref_triton_fwd_ms": REF_TRITON_FWD_MS.get(T), "ref_triton_fwd_peak_mb": REF_TRITON_FWD_MB.get(T),
+               "ref_triton_fwd_bwd_peak_mb": REF_TRITON_FWDBWD_MB.get(T)}
+        row["fwd_speedup_vs_ref_published"] = round(REF_TRITON_FWD_MS[T] / ms, 2)
+        rows.append(row)
+        del x, xg
+    torch.cuda.empty_cache()
+    return {"workload": "reference benchmarks/bench_triton.py: ScreeningAttention(512, 8, causal) module forward, "
+                        "fp32, B=4, s_r=-2 (r=1.135), default windows",
+            "ref_hardware": "RTX 4060 Ti (BENCHMARK_REPORT_TRITON.md:61-85; a different GPU)",
+            "rows": rows}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -386,9 +557,38 @@ def main():
         grads = ops.bwd_raw(q, k, v, rg, wg, True, 1e-8, y, hnorm, bits, dy)
         return bits
 
+    # The supplementary legs run first: a few seconds of GPU work, after which
+    # the headline below runs at the clocks the GPU holds under sustained
+    # work (from a cold start the first ~50 ms of steps run up to 8% slower).
+    # The headline's own warm-up is still exactly `warmup` steps.
+    extra = {}
+    if not args.no_configs:
+        legs = (("cfg3_lm_train_step", lambda: cfg3_bench(L, torch)),
+                ("cfg4_prefill_100k", lambda: cfg4_bench(L, ops, torch)),
+                ("cfg5_decode_literal", lambda: cfg5_bench(torch)),
+                ("cfg2_trained_regime", lambda: trained_regime_bench(L, ops, torch)),
+                ("cfg2_f16", lambda: fp16_bench(L, ops, torch, q, k, v, dy, r, w)),
+                ("ref_fused_module_fwd", lambda: ref_module_bench(torch)))
+        for key, leg in legs:
+            try:
+                extra[key] = leg()
+            except Exception as e:  # reported in the line, not hidden
+                extra[key] = {"error": f"{type(e).__name__}: {e}"}
+            torch.cuda.empty_cache()
+    if not args.no_decode:
+        extra["decode"] = decode_bench(L, ops, torch)
+        torch.cuda.empty_cache()
+
     for _ in range(args.warmup):
         bits = step()
     torch.cuda.synchronize()
+    # peak device memory of one step (inputs resident; outputs, workspaces,
+    # bitmap and gradients allocated by the step)
+    torch.cuda.reset_peak_memory_stats()
+    base_mb = torch.cuda.memory_allocated() / 1e6
+    step()
+    torch.cuda.synchronize()
+    peak_mb = torch.cuda.max_memory_allocated() / 1e6
 
     # per-kernel breakdown (HIP events around each launch, outside the timed
     # region) picks the dominant kernel; its launches are then timed again
@@ -470,18 +670,11 @@ def main():
                           "launch gap (about 1-3 us), so they sum past ms_per_step; profiles/ has the "
                           "rocprofv3 durations",
         "wall_s_timed": round(wall, 3),
+        "peak_memory_mb": {"step": round(peak_mb, 1), "inputs_resident": round(base_mb, 1),
+                           "note": "torch.cuda.max_memory_allocated over one fwd+bwd step; inputs_resident "
+                                   "is q, k, v, dO and r, w before it"},
     }
-    if not args.no_decode:
-        out["decode"] = decode_bench(L, ops, torch)
-    if not args.no_configs:
-        for key, leg in (("cfg3_lm_train_step", lambda: cfg3_bench(L, torch)),
-                         ("cfg4_prefill_100k", lambda: cfg4_bench(L, ops, torch)),
-                         ("cfg5_decode_literal", lambda: cfg5_bench(torch))):
-            try:
-                out[key] = leg()
-            except Exception as e:  # reported in the line, not hidden
-                out[key] = {"error": f"{type(e).__name__}: {e}"}
-            torch.cuda.empty_cache()
+    out.update(extra)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, H, D, r, w, args.seed)
     if args.calib_copy:

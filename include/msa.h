@@ -20,7 +20,7 @@
  *             proj(x).view(B,T,H,D) view the reference builds before its
  *             transpose (attention.py:150-153).  Strides and base pointers
  *             must allow 16-byte vector loads (strides multiple of 8 elements
- *             for bf16, of 4 for fp32).
+ *             for bf16 and fp16, of 4 for fp32).
  *   y, dy, dq, dk, dv : contiguous (B, T, H, D), i.e. the (B,T,d_model) layout
  *             out_proj consumes (attention.py:198-200).
  *   r, w    : fp32 (H,), r = exp(s_r)+1, w = exp(s_v)+1 (attention.py:164-165).
@@ -29,7 +29,10 @@
  *             when r >= 1.  A window that is NaN or not positive is treated as
  *             empty (zero output for that head; the reference gives NaN).
  *   key_padding_mask : nullable uint8 (B, Tk), nonzero = ignore key.
- *   dtype   : MSA_F32 or MSA_BF16 for q,k,v,y,dy,dq,dk,dv.
+ *   dtype   : MSA_F32, MSA_BF16 or MSA_F16 for q,k,v,y,dy,dq,dk,dv (the
+ *             reference's fused forward takes float16 or float32 operands,
+ *             screening_fwd.py:235; torch.autocast("cuda") gives float16).
+ *             bf16 and fp16 run on the 32x32x16 MFMA with fp32 accumulation.
  *   dropout_p, dropout_seed : attention dropout on alpha*m (attention.py:68,
  *             :190, nn.Dropout in training mode), 0 <= p < 1; p = 0 is the
  *             identity.  The keep decision of pair (b, h, i, j) is a
@@ -61,7 +64,7 @@
 extern "C" {
 #endif
 
-enum msa_dtype { MSA_F32 = 0, MSA_BF16 = 1 };
+enum msa_dtype { MSA_F32 = 0, MSA_BF16 = 1, MSA_F16 = 2 };
 
 enum msa_status {
   MSA_OK = 0,
@@ -70,7 +73,9 @@ enum msa_status {
   MSA_ERR_HIP = 3        /* a HIP runtime call or kernel launch failed      */
 };
 
-/* Library version, (major<<16)|(minor<<8)|patch. */
+/* Library version, (major<<16)|(minor<<8)|patch.  0.2.0 inserted window_hint
+ * before r in msa_decode / msa_decode_at (a binary built against 0.1.0 must
+ * be rebuilt); 0.3.0 added MSA_F16. */
 int msa_version(void);
 
 /* Thread-local text of the last error raised on this thread ("" if none). */

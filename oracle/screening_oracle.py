@@ -395,7 +395,8 @@ def live_pairs(q, k, r, w, causal=True, eps=EPS, key_padding_mask=None, block=10
                 if hi <= lo:
                     continue
                 s32 = qn32[b, hh, i0:i1] @ kn32[b, hh, lo:hi].T
-                ii, jj = np.nonzero(s32 > np.float32(thr - SCREEN_MARGIN))
+                # flat indices: one pass over a mostly-false mask
+                ii, jj = np.divmod(np.flatnonzero(s32 > np.float32(thr - SCREEN_MARGIN)), hi - lo)
                 ii = ii.astype(np.int64) + i0
                 jj = jj.astype(np.int64) + lo
                 rel = ii - jj                       # i - j
@@ -420,7 +421,9 @@ def sparse_forward_backward(q, k, v, r, w, dy=None, causal=True, eps=EPS, key_pa
     """forward() and, when dy is given, backward() evaluated over the live pairs only.
 
     Returns (y, grads, pairs): y (B,Tq,H,D); grads = (dq, dk, dv, dr, dw) as
-    backward() returns them, or None without dy; pairs = live_pairs(...).
+    backward() returns them, or None without dy; pairs = live_pairs(...),
+    with dy also "dr_abs" and "dw_abs" (H,): the per-head sums of the absolute
+    values of the terms that dr and dw sum.
     Same math and conventions as forward()/backward(), float64 throughout."""
     import scipy.sparse as sp
     if pairs is None:
@@ -465,8 +468,12 @@ def sparse_forward_backward(q, k, v, r, w, dy=None, causal=True, eps=EPS, key_pa
     dqn = np.asarray(DS @ kf).reshape(B, H, Tq, D)
     dkn = np.asarray(DS.T @ qf).reshape(B, H, Tk, D)
     dvn = np.asarray(P.T @ dh).reshape(B, H, Tk, D)
-    dr = np.bincount(ph, weights=-2.0 * a * (1.0 - s) * m * dP, minlength=H)
-    dw = np.bincount(ph, weights=a * a * mdw * dP, minlength=H)
+    tr, tw = -2.0 * a * (1.0 - s) * m * dP, a * a * mdw * dP
+    dr = np.bincount(ph, weights=tr, minlength=H)
+    dw = np.bincount(ph, weights=tw, minlength=H)
+    # per-head sums of |term|: the scale a per-head sum's rounding error has
+    pairs["dr_abs"] = np.bincount(ph, weights=np.abs(tr), minlength=H)
+    pairs["dw_abs"] = np.bincount(ph, weights=np.abs(tw), minlength=H)
     t = lambda x: np.transpose(x, (0, 2, 1, 3))
     grads = (t(_normalize_bwd(qh, dqn, eps)), t(_normalize_bwd(kh, dkn, eps)),
              t(_normalize_bwd(vh, dvn, eps)), dr, dw)

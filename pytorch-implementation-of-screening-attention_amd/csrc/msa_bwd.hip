@@ -358,11 +358,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
     }
     // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
     // the key rows, one 32-column block of d at a time
-    {
-      float sc[16];
-      read_row_scales(sk, half, sc);
+    // (fp16: the K^T rows take 1/|k| instead, below)
+    float ksc[16];
+    read_row_scales(sk, half, ksc);
+    if constexpr (!kScaleRowsNotWeights<T>) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
+      for (int r = 0; r < 16; ++r) dp[r] *= ksc[r];
     }
     frag db[NC];
 #pragma unroll
@@ -378,6 +379,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
       for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) tr = M::mma_ng(kc[dblk * NC + c], id[c], tr);
+      if constexpr (kScaleRowsNotWeights<T>) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tr[r] *= ksc[r];
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) kt[c] = M::pack(tr, c * PER);
 #pragma unroll
@@ -606,11 +611,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
       for (int r = 0; r < 16; ++r)
         if (((pm0 >> r) & 1u) == 0u) { s[r] = 0.0f; dp[r] = 0.0f; }
     }
-    {
-      float sc[16];
-      read_row_scales(sq, half, sc);
+    // ds/|q| (fp16: the Q^T rows take 1/|q| instead, below)
+    float qsc[16];
+    read_row_scales(sq, half, qsc);
+    if constexpr (!kScaleRowsNotWeights<T>) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] *= sc[r];  // ds/|q|
+      for (int r = 0; r < 16; ++r) dp[r] *= qsc[r];
     }
     // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
     // with dH^T, Q^T from identity products on the row registers, one
@@ -633,6 +639,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
 #pragma unroll
         for (int c = 0; c < NC; ++c)
           tr = M::mma_ng(op == 0 ? hf[dblk * NC + c] : qf[dblk * NC + c], id[c], tr);
+        if constexpr (kScaleRowsNotWeights<T>) {
+          if (op == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tr[r] *= qsc[r];
+          }
+        }
 #pragma unroll
         for (int c = 0; c < NC; ++c) t[c] = M::pack(tr, c * PER);
 #pragma unroll
@@ -714,6 +726,11 @@ hipError_t launch_bwd(const BwdCall& c) {
     if (DP == 32) return launch_bwd_t<bf16, 32>(c);
     if (DP == 64) return launch_bwd_t<bf16, 64>(c);
     return launch_bwd_t<bf16, 128>(c);
+  }
+  if (c.g.dtype == 2) {
+    if (DP == 32) return launch_bwd_t<f16, 32>(c);
+    if (DP == 64) return launch_bwd_t<f16, 64>(c);
+    return launch_bwd_t<f16, 128>(c);
   }
   if (DP == 32) return launch_bwd_t<float, 32>(c);
   if (DP == 64) return launch_bwd_t<float, 64>(c);

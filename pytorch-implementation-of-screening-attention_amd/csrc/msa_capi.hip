@@ -40,7 +40,8 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Shared shape validation; fills g on success.
 int check_geometry(int B, int H, int Tq, int Tk, int D, int dtype, int causal, msa::Geometry* g) {
-  if (dtype != MSA_F32 && dtype != MSA_BF16) return fail(MSA_ERR_INVALID, "dtype must be MSA_F32 or MSA_BF16");
+  if (dtype != MSA_F32 && dtype != MSA_BF16 && dtype != MSA_F16)
+    return fail(MSA_ERR_INVALID, "dtype must be MSA_F32, MSA_BF16 or MSA_F16");
   if (!(D == 16 || D == 32 || D == 64 || D == 128))
     return fail(MSA_ERR_INVALID, "head_dim D=%d unsupported (16, 32, 64 or 128)", D);
   if (B < 0 || H <= 0 || Tq < 0 || Tk < 0) return fail(MSA_ERR_INVALID, "negative or zero size");
@@ -51,20 +52,20 @@ int check_geometry(int B, int H, int Tq, int Tk, int D, int dtype, int causal, m
   g->nqt = msa::ntiles(Tq); g->nkt = msa::ntiles(Tk);
   g->nku_words = (2 * g->nkt + 31) / 32;
   g->Tq_pad = (int64_t)g->nqt * 64; g->Tk_pad = (int64_t)g->nkt * 64;
-  g->esize = dtype == MSA_BF16 ? 2 : 4;
+  g->esize = dtype == MSA_F32 ? 4 : 2;
   return MSA_OK;
 }
 
 int check_tensor(const char* name, const void* p, int64_t sb, int64_t st, int64_t sh, int dtype) {
   if (p == nullptr) return fail(MSA_ERR_INVALID, "%s is null", name);
   if (!aligned16(p)) return fail(MSA_ERR_INVALID, "%s is not 16-byte aligned", name);
-  const int64_t m = dtype == MSA_BF16 ? 8 : 4;
+  const int64_t m = dtype == MSA_F32 ? 4 : 8;
   if (sb < 0 || st < 0 || sh < 0 || sb % m || st % m || sh % m)
     return fail(MSA_ERR_INVALID, "%s strides (%lld,%lld,%lld) must be non-negative multiples of %lld elements", name,
                 (long long)sb, (long long)st, (long long)sh, (long long)m);
   // kernels address the rows of a 64-row tile by 32-bit byte offsets from the
   // tile's first row
-  const int64_t es = dtype == MSA_BF16 ? 2 : 4;
+  const int64_t es = dtype == MSA_F32 ? 4 : 2;
   if (st * 64 * es >= (int64_t)1 << 32)
     return fail(MSA_ERR_INVALID, "%s time stride %lld elements is too large (64 rows must span < 4 GiB)", name,
                 (long long)st);
@@ -172,7 +173,9 @@ int msa_timer_read(int kernel, float* ms, int n) {
 }
 
 
-int msa_version(void) { return (0 << 16) | (1 << 8) | 0; }
+// 0.1.0: first release; 0.2.0: msa_decode and msa_decode_at take window_hint
+// (an argument inserted before r); 0.3.0: MSA_F16.
+int msa_version(void) { return (0 << 16) | (3 << 8) | 0; }
 
 const char* msa_last_error(void) { return g_last_error.c_str(); }
 

@@ -64,6 +64,12 @@ template <> struct Vec16<bf16> {
   __device__ static inline float dot(const type& a, const type& b, float acc) { return frag_dot(a, b, acc); }
   __device__ static inline float get(const type& a, int e) { return (float)a[e]; }
 };
+template <> struct Vec16<f16> {
+  typedef f16x8 type;
+  static constexpr int N = 8;
+  __device__ static inline float dot(const type& a, const type& b, float acc) { return frag_dot(a, b, acc); }
+  __device__ static inline float get(const type& a, int e) { return (float)a[e]; }
+};
 template <> struct Vec16<float> {
   typedef f32x4 type;
   static constexpr int N = 4;
@@ -359,6 +365,14 @@ hipError_t launch_decode(const DecodeCall& c) {
       case 32: return launch_decode_t<bf16, 32>(c);
       case 64: return launch_decode_t<bf16, 64>(c);
       default: return launch_decode_t<bf16, 128>(c);
+    }
+  }
+  if (c.dtype == 2) {
+    switch (c.D) {
+      case 16: return launch_decode_t<f16, 16>(c);
+      case 32: return launch_decode_t<f16, 32>(c);
+      case 64: return launch_decode_t<f16, 64>(c);
+      default: return launch_decode_t<f16, 128>(c);
     }
   }
   switch (c.D) {

@@ -11,6 +11,9 @@ namespace msa {
 typedef __bf16 bf16;
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef _Float16 f16;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
@@ -103,6 +106,42 @@ template <> struct Mma<bf16> {
     return f;
   }
 };
+
+// fp16: the same 32x32x16 operand layout and pass count as bf16
+// (v_mfma_f32_32x32x16_f16), so every layout map and the source-operand guard
+// apply unchanged.
+template <> struct Mma<f16> {
+  static constexpr int KS = 16;
+  static constexpr int PER = 8;
+  typedef f16x8 frag;
+  __device__ static inline f32x16 mma(frag a, frag b, f32x16 c) {
+    const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    guard_mfma_sources(a, b);
+    return d;
+  }
+  __device__ static inline f32x16 mma_ng(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline frag load(const f16* p) { return *reinterpret_cast<const frag*>(p); }
+  __device__ static inline frag zero() { frag z; for (int e = 0; e < 8; ++e) z[e] = (f16)0.0f; return z; }
+  __device__ static inline float get(const frag& f, int e) { return (float)f[e]; }
+  __device__ static inline frag pack(const f32x16& c, int r0) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (f16)c[r0 + e];
+    return f;
+  }
+};
+
+// Where a per-row factor 1/|x| enters a product whose other operand is
+// packed to the input type.  bf16 (8 exponent bits) folds it into the pair
+// weights (alpha*m/|v|, ds/|k|, ds/|q|) and keeps the raw rows exact.  fp16
+// has 5 exponent bits: a weight times 1/|x| overflows to inf for rows shorter
+// than about 1.5e-5 (a zero row gives 1/eps = 1e8, then inf * 0 = NaN), so
+// the fp16 kernels scale the transposed rows instead (x^ = x/|x|, at most 1
+// in magnitude) and the weights stay at most 2r|dP|.
+template <typename T>
+constexpr bool kScaleRowsNotWeights = sizeof(T) == 2 && !__is_same(T, bf16);
 
 template <> struct Mma<float> {
   static constexpr int KS = 2;
@@ -301,9 +340,11 @@ __device__ inline typename Mma<T>::frag load_or_zero(const T* p, bool ok) {
 
 __device__ inline float to_f(float x) { return x; }
 __device__ inline float to_f(bf16 x) { return (float)x; }
+__device__ inline float to_f(f16 x) { return (float)x; }
 template <typename T> __device__ inline T from_f(float x);
 template <> __device__ inline float from_f<float>(float x) { return x; }
 template <> __device__ inline bf16 from_f<bf16>(float x) { return (bf16)x; }
+template <> __device__ inline f16 from_f<f16>(float x) { return (f16)x; }
 
 // Stores 4 consecutive values.
 __device__ inline void store4(float* p, float a, float b, float c, float d) {
@@ -312,12 +353,21 @@ __device__ inline void store4(float* p, float a, float b, float c, float d) {
 __device__ inline void store4(bf16* p, float a, float b, float c, float d) {
   *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a, (bf16)b, (bf16)c, (bf16)d};
 }
-// Stores 8 consecutive values (16 bytes for bf16).
+__device__ inline void store4(f16* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f16x4*>(p) = f16x4{(f16)a, (f16)b, (f16)c, (f16)d};
+}
+// Stores 8 consecutive values (16 bytes for bf16 and fp16).
 __device__ inline void store8(bf16* p, const float (&v)[8]) {
   bf16x8 o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
   *reinterpret_cast<bf16x8*>(p) = o;
+}
+__device__ inline void store8(f16* p, const float (&v)[8]) {
+  f16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (f16)v[e];
+  *reinterpret_cast<f16x8*>(p) = o;
 }
 __device__ inline void store8(float* p, const float (&v)[8]) {
   *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
@@ -359,6 +409,10 @@ __device__ inline f32x4 load4(const bf16* p) {
   bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
   return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
+__device__ inline f32x4 load4(const f16* p) {
+  f16x4 v = *reinterpret_cast<const f16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
 
 __device__ inline int64_t floordiv(int64_t a, int64_t b) {  // b > 0
   return a >= 0 ? a / b : -((-a + b - 1) / b);
@@ -379,6 +433,16 @@ __device__ inline float frag_dot(const bf16x8& a, const bf16x8& b, float acc) {
   for (int e = 0; e < 8; e += 2) {
     const bf16x2_t x = {a[e], a[e + 1]}, y = {b[e], b[e + 1]};
     acc = __builtin_amdgcn_fdot2_f32_bf16(x, y, acc, false);
+  }
+  return acc;
+}
+// fp16: v_dot2_f32_f16, two products per instruction accumulated in fp32.
+__device__ inline float frag_dot(const f16x8& a, const f16x8& b, float acc) {
+  typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const f16x2_t x = {a[e], a[e + 1]}, y = {b[e], b[e + 1]};
+    acc = __builtin_amdgcn_fdot2(x, y, acc, false);
   }
   return acc;
 }

@@ -15,7 +15,8 @@
 //                   trim-and-square threshold (attention.py:75-90).  Output:
 //                   the live-unit bitmap (32x32 units).
 //   fwd_live_kernel : one wave per 32-query unit; walks the unit's live bits,
-//                   recomputes S^T for those key units only, forms alpha*m
+//                   recomputes S^T from the raw K rows (exact products, fp32
+//                   1/|k|) for those key units only, forms alpha*m
 //                   (attention.py:92-119) and accumulates H^T += V^T P^T with
 //                   1/|v_j| folded into P.  The epilogue applies TanhNorm
 //                   (norm.py:23-25) and writes y in (B,T,H,D) and |h| per row.
@@ -337,7 +338,9 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
 
 struct FwdKArgs {
   const void* q; Strides3 qs;
+  const void* k; Strides3 ks;
   const void* v; Strides3 vs;
+  const uint8_t* kpm;
   const void* khat;
   const float* r; const float* w;
   void* y; float* hnorm; uint32_t* bits;
@@ -670,11 +673,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // Live units.  One wave (a 64-thread block) per query unit: 32 consecutive
 // queries of one head, lane -> query i = 32*qu + l%32.  The wave walks its
 // row of the live-unit bitmap; for each live key unit (32 keys) it loads the
-// K^ rows (workspace) and raw V rows straight from global memory as MFMA
-// operands, the next unit's loads in flight while the current one is
-// computed: S^T from K^ (the screen's operands and order, so the same
-// values), alpha*m (attention.py:92-119) with 1/|v_j| folded in, and
-// H^T += V^T P^T with V^T from an identity MFMA on the raw V rows.  The
+// raw K and V rows straight from global memory as MFMA operands, the next
+// unit's loads in flight while the current one is computed: S^T = K Q^T on
+// the raw values (exact products, as the backward forms it) scaled by
+// 1/|k_j| in fp32, alpha*m (attention.py:92-119) with 1/|v_j| folded in
+// (fp16: into the V rows), and H^T += V^T P^T with V^T from an identity MFMA
+// on the raw V rows.  The
 // epilogue applies TanhNorm (norm.py:23-25) and writes y in (B,T,H,D) and |h|
 // per row.  Units with no live key unit get y = 0, |h| = 0.
 // ---------------------------------------------------------------------------
@@ -685,6 +689,7 @@ void fwd_live_kernel(FwdKArgs a) {
   using frag = typename M::frag;
   using R = PRow<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
+  __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k_j| (0 if padded or masked) of the current unit
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
@@ -723,31 +728,30 @@ void fwd_live_kernel(FwdKArgs a) {
 
   // key row of this lane in unit u: 32u + perm_row(l32) (A-operand order)
   const int m = perm_row(l32);
-  const T* kg = (const T*)a.khat + (int64_t)bh * a.Tk_pad * DP;
+  const T* kg = (const T*)a.k + b * a.ks.sb + h * a.ks.sh;
   const T* vg = (const T*)a.v + b * a.vs.sb + h * a.vs.sh;
-  // The lane's chunks (elements KS*ks + PER*half) of its row of key unit u,
-  // from one row address and immediate offsets.  K^ rows exist up to Tk_pad
-  // (zero past Tk and for masked keys, so those keys never pass the
-  // threshold and their P is exactly 0); V rows past Tk read row Tk-1
-  // instead, which P = 0 then cancels.  Only D = 16 < DP has chunks past D,
-  // and they hold zeros.
-  // Addresses: a wave-uniform 64-bit unit base plus a 32-bit lane offset.
-  const uint32_t koff = (uint32_t)((m * DP + PER * half) * (int)sizeof(T));
-  auto load_k = [&](int u, frag (&f)[NKS]) {
-    const char* p = (const char*)(kg + (int64_t)u * kUnit * DP) + koff;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) f[ks] = M::load((const T*)(p + KS * ks * (int)sizeof(T)));
-  };
-  auto load_v = [&](int u, frag (&f)[NKS]) {
+  // The lane's chunks (elements KS*ks + PER*half) of its raw K or V row of
+  // key unit u, from one row address and immediate offsets: a wave-uniform
+  // 64-bit unit base plus a 32-bit lane offset.  Rows past Tk read row Tk-1
+  // instead; their 1/|k| is 0 (as for masked keys), so they never pass the
+  // threshold and their P is exactly 0.  Only D = 16 < DP has chunks past D
+  // (they re-read chunk 0; vzero clears them).
+  auto load_rows = [&](const T* base, int64_t st, int u, frag (&f)[NKS]) {
     const int r = u * kUnit + m < a.Tk ? m : a.Tk - 1 - u * kUnit;
-    const uint32_t off = (uint32_t)(((int64_t)r * a.vs.st + PER * half) * (int64_t)sizeof(T));
-    const char* p = (const char*)(vg + (int64_t)u * kUnit * a.vs.st) + off;
-    // chunks past D (D = 16 < DP = 32 only) re-read chunk 0; vzero clears them
+    const uint32_t off = (uint32_t)(((int64_t)r * st + PER * half) * (int64_t)sizeof(T));
+    const char* p = (const char*)(base + (int64_t)u * kUnit * st) + off;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int c = DP == 32 && KS * ks >= a.D ? 0 : KS * ks;
       f[ks] = M::load((const T*)(p + c * (int)sizeof(T)));
     }
+  };
+  auto load_k = [&](int u, frag (&f)[NKS]) { load_rows(kg, a.ks.st, u, f); };
+  auto load_v = [&](int u, frag (&f)[NKS]) { load_rows(vg, a.vs.st, u, f); };
+  // 1/|k| is 0 for keys past Tk and for masked keys
+  auto key_ok = [&](int u) {
+    const int j = u * kUnit + m;
+    return j < a.Tk && !(a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + j] != 0);
   };
   auto vzero = [&](frag (&f)[NKS]) {
     if constexpr (DP == 32) {
@@ -761,16 +765,18 @@ void fwd_live_kernel(FwdKArgs a) {
   frag qf[NKS];
   float iq;
   frag kc[NKS], vc[NKS];
+  bool kok;
   {
     R qr;
     qr.load((const T*)a.q + b * a.qs.sb + (int64_t)(valid ? i : 0) * a.qs.st + h * a.qs.sh, valid, a.D, half);
     load_k(cur, kc);
     load_v(cur, vc);
+    kok = key_ok(cur);
     iq = qr.inv_norm(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
   }
-  const float thq = hp.thr / iq;  // s > thr  <=>  k^ . q > thr |q|
+  const float thq = hp.thr / iq;  // s > thr  <=>  (k . q)/|k| > thr |q|
   f32x16 o[NDH];
 #pragma unroll
   for (int dblk = 0; dblk < NDH; ++dblk)
@@ -779,17 +785,27 @@ void fwd_live_kernel(FwdKArgs a) {
 
   for (;;) {
     const int k0 = cur * kUnit;
-    // S^T: register r -> key k0 + rowof(r, half), lane -> query i
+    // S^T = K Q^T on the raw rows (exact products of the inputs, fp32
+    // accumulation), scaled by 1/|k_j| in fp32 below: register r -> key
+    // k0 + rowof(r, half), lane -> query i
+    vzero(kc);
     f32x16 s;
+    float s2k = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
     if constexpr (sizeof(T) == 2) {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s = M::mma_ng(kc[ks], qf[ks], s);
+      for (int ks = 0; ks < NKS; ++ks) {
+        s = M::mma_ng(kc[ks], qf[ks], s);
+        s2k = frag_dot(kc[ks], kc[ks], s2k);
+      }
       guard_frags(kc);
     } else {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s = M::mma(kc[ks], qf[ks], s);
+      for (int ks = 0; ks < NKS; ++ks) {
+        s = M::mma(kc[ks], qf[ks], s);
+        s2k = frag_dot(kc[ks], kc[ks], s2k);
+      }
     }
     // each operand's registers take the next unit's rows as soon as they are
     // free, so those loads run behind the rest of this unit's work (past the
@@ -797,24 +813,39 @@ void fwd_live_kernel(FwdKArgs a) {
     // waits for the same count)
     const int nxt = walk.next();
     const int nl = nxt >= 0 ? nxt : cur;
+    const bool kok_c = kok;
     load_k(nl, kc);
-    // 1/|v_j| of the lane's key row, to LDS (read back in register order
-    // where a pair passes), then V^T by identity MFMA
+    kok = key_ok(nl);
+    // 1/|k_j| and 1/|v_j| of the lane's key row, to LDS (read back in
+    // register order), then V^T by identity MFMA
     vzero(vc);
     {
-      float s2 = 0.0f;
+      float s2v = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s2 = frag_dot(vc[ks], vc[ks], s2);
-      s2 = half_sum(s2);
-      const float iv = inv_len(s2, a.eps);
+      for (int ks = 0; ks < NKS; ++ks) s2v = frag_dot(vc[ks], vc[ks], s2v);
+      s2v = half_sum(s2v);
+      s2k = half_sum(s2k);
+      const float iv = inv_len(s2v, a.eps);
+      const float ik = kok_c ? inv_len(s2k, a.eps) : 0.0f;
       wave_lds_sync();
-      if (half == 0) sv[m] = iv;
+      if (half == 0) {
+        sv[m] = iv;
+        sk[m] = ik;
+      }
       wave_lds_sync();
+    }
+    {
+      float ksc[16];
+      read_row_scales(sk, half, ksc);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] *= ksc[r];
     }
     frag ta[NDH * NC];
     frag id[NC];  // formed per unit: fewer registers held across the loop
 #pragma unroll
     for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
+    float vsc[16];  // fp16: 1/|v_j| of the transposed rows (register order)
+    if constexpr (kScaleRowsNotWeights<T>) read_row_scales(sv, half, vsc);
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk) {
       f32x16 tr;
@@ -822,6 +853,10 @@ void fwd_live_kernel(FwdKArgs a) {
       for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) tr = M::mma_ng(vc[dblk * NC + c], id[c], tr);
+      if constexpr (kScaleRowsNotWeights<T>) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tr[r] *= vsc[r];
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr, c * PER);
     }
@@ -838,7 +873,8 @@ void fwd_live_kernel(FwdKArgs a) {
         const float av = trim(s[r] * iq, hp.r);
         float p = 0.0f;
         if (av > 0.0f && in_window(dd, hp)) {
-          p = av * av * softmask(dd, hp.iw) * sv[rowof(r, half)];
+          p = av * av * softmask(dd, hp.iw);
+          if constexpr (!kScaleRowsNotWeights<T>) p *= sv[rowof(r, half)];
           if (a.drop.on) p *= dropout_factor(a.drop, bh, i, i - dd);
         }
         s[r] = p;
@@ -891,7 +927,8 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
   screen_plan_dims(g, plan.seg, plan.kmax, plan.per_xcd);
   plan.table = (ScreenItem*)((char*)c.khat + khat_bytes(g));
   FwdKArgs fa;
-  fa.q = c.q; fa.qs = c.qs; fa.v = c.v; fa.vs = c.vs; fa.khat = c.khat;
+  fa.q = c.q; fa.qs = c.qs; fa.k = c.k; fa.ks = c.ks; fa.v = c.v; fa.vs = c.vs; fa.kpm = c.kpm;
+  fa.khat = c.khat;
   fa.r = c.r; fa.w = c.w; fa.y = c.y; fa.hnorm = c.hnorm; fa.bits = c.bits;
   fa.H = g.H; fa.Tq = g.Tq; fa.Tk = g.Tk; fa.D = g.D; fa.nqt = g.nqt; fa.nku_words = g.nku_words;
   fa.causal = g.causal; fa.Tk_pad = g.Tk_pad; fa.eps = c.eps; fa.drop = c.drop;
@@ -934,6 +971,11 @@ hipError_t launch_fwd(const FwdCall& c) {
     if (DP == 32) return launch_fwd_t<bf16, 32>(c);
     if (DP == 64) return launch_fwd_t<bf16, 64>(c);
     return launch_fwd_t<bf16, 128>(c);
+  }
+  if (c.g.dtype == 2) {
+    if (DP == 32) return launch_fwd_t<f16, 32>(c);
+    if (DP == 64) return launch_fwd_t<f16, 64>(c);
+    return launch_fwd_t<f16, 128>(c);
   }
   if (DP == 32) return launch_fwd_t<float, 32>(c);
   if (DP == 64) return launch_fwd_t<float, 64>(c);

@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmsa.so")
 
 MSA_F32 = 0
 MSA_BF16 = 1
+MSA_F16 = 2
 
 # kernel ids for msa_timer_arm (include/msa.h)
 K_PREP_K, K_FWD_SCREEN, K_FWD_LIVE, K_DKDV, K_DQ, K_DECODE = 1, 2, 3, 4, 5, 7

@@ -74,23 +74,18 @@ class ScreeningAttention(nn.Module):
         """proj(x) viewed as (B, T, H, D) -- no copy (attention.py:150-151)."""
         return proj(x).view(x.shape[0], x.shape[1], self.num_heads, self.head_dim)
 
-    def _fused_weight(self, projs) -> torch.Tensor:
-        """The projections' weights stacked along the output dimension.  Under
-        autograd the concatenation is part of the graph (its backward splits
-        the gradient back to each Linear); without it the stacked weight is
-        kept and rebuilt only when a weight changes (in-place updates bump
-        their version counters)."""
-        ws = [p.weight for p in projs]
-        if torch.is_grad_enabled():
-            return torch.cat(ws)
-        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
-        cache = self.__dict__.get("_fused_cache", {})
-        hit = cache.get(len(ws))
-        if hit is None or hit[0] != key:
-            hit = (key, torch.cat(ws))
-            cache[len(ws)] = hit
-            self.__dict__["_fused_cache"] = cache
-        return hit[1]
+    @staticmethod
+    def _plain(projs) -> bool:
+        """True when every projection is a bias-free nn.Linear with no forward
+        hooks (its own or global): only then does one GEMM over the stacked
+        weights give exactly what calling the modules gives.  Anything else
+        (hooks such as weight_norm or LoRA wrappers, subclasses, a bias) takes
+        the per-module calls of attention.py:150-153."""
+        from torch.nn.modules import module as _m
+        if _m._global_forward_hooks or _m._global_forward_pre_hooks:
+            return False
+        return all(type(p) is nn.Linear and p.bias is None and not p._forward_hooks
+                   and not p._forward_pre_hooks for p in projs)
 
     def project_qkv(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor):
         """q, k, v projections as (B, T, H, D) views (attention.py:147-153) from
@@ -98,18 +93,19 @@ class ScreeningAttention(nn.Module):
         for self-attention (query is key is value), one for q and one over the
         stacked k/v weights when key is value (cross-attention over a memory),
         else three.  The views' time stride is then 3*d_model (or 2*d_model);
-        the fused kernels read them in place."""
+        the fused kernels read them in place.  The stacked weight is formed on
+        every call (a copy of 2-3 d x d weights), so weight updates of any kind,
+        in place or through .data, are always seen."""
         B, Tq, _ = query.shape
         Tk = key.shape[1]
         H, D, d = self.num_heads, self.head_dim, self.d_model
-        if query is key and key is value:
-            qkv = F.linear(query, self._fused_weight((self.q_proj, self.k_proj, self.v_proj)))
-            q, k, v = qkv.split(d, dim=-1)
+        if query is key and key is value and self._plain((self.q_proj, self.k_proj, self.v_proj)):
+            wqkv = torch.cat((self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+            q, k, v = F.linear(query, wqkv).split(d, dim=-1)
             return q.view(B, Tq, H, D), k.view(B, Tq, H, D), v.view(B, Tq, H, D)
         q = self.project(query, self.q_proj)
-        if key is value:
-            kv = F.linear(key, self._fused_weight((self.k_proj, self.v_proj)))
-            k, v = kv.split(d, dim=-1)
+        if key is value and self._plain((self.k_proj, self.v_proj)):
+            k, v = F.linear(key, torch.cat((self.k_proj.weight, self.v_proj.weight))).split(d, dim=-1)
             return q, k.view(B, Tk, H, D), v.view(B, Tk, H, D)
         return q, self.project(key, self.k_proj), self.project(value, self.v_proj)
 
@@ -182,7 +178,6 @@ class ScreeningAttention(nn.Module):
             return self.out_proj(y.reshape(B, 1, self.d_model))
         cache.store(k, v, pos)
         if x.is_cuda:
-            # the cache's dtype is the kernel's (fp16 models keep an fp32 cache)
             y = ops.decode_step(q[:, 0].to(cache.k.dtype), cache.k, cache.v, pos + 1, r, w, self.eps,
                                 cache.workspace, cache.window_hint).to(x.dtype)
         else:
@@ -196,12 +191,10 @@ class KVCache:
 
     Stored head-major, (B, H, capacity, D), so that one head's window is one
     contiguous stream for the decode kernel; `k` and `v` are the (B, capacity,
-    H, D) views of that storage, the layout of the projections.  The kernels
-    compute in float32 or bfloat16, so a float16 model's cache is float32."""
+    H, D) views of that storage, the layout of the projections, in the model's
+    dtype (float32, bfloat16 or float16)."""
 
     def __init__(self, batch, capacity, num_heads, head_dim, dtype, device, window_hint=0):
-        if dtype == torch.float16:
-            dtype = torch.float32
         # 0, or a bound on ceil(w) over the layer's heads: sizes the decode
         # launch to the windows instead of the cache (results do not depend on it)
         self.window_hint = int(window_hint)

@@ -22,7 +22,7 @@ import torch
 
 from . import _native
 
-_DTYPES = {torch.float32: _native.MSA_F32, torch.bfloat16: _native.MSA_BF16}
+_DTYPES = {torch.float32: _native.MSA_F32, torch.bfloat16: _native.MSA_BF16, torch.float16: _native.MSA_F16}
 
 
 def _stream_ptr(device):
@@ -65,7 +65,7 @@ def _dropout_args(dropout_p, seed):
 def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, dropout_p=0.0, seed=0):
     """One msa_fwd call.  Returns (y, hnorm, tile_bits).
 
-    q (B,Tq,H,D), k/v (B,Tk,H,D) in float32 or bfloat16 on one GPU; r, w (H,).
+    q (B,Tq,H,D), k/v (B,Tk,H,D) in float32, bfloat16 or float16 on one GPU; r, w (H,).
     dropout_p / seed: attention dropout with the counter-based keep mask that
     include/msa.h defines (p = 0: none).
     """
@@ -73,7 +73,7 @@ def fwd_raw(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, dropout
     if not q.is_cuda:
         raise RuntimeError("screening_core runs on the GPU only (got a CPU tensor)")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise TypeError(f"q/k/v must share dtype float32 or bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+        raise TypeError(f"q/k/v must share dtype float32, bfloat16 or float16, got {q.dtype}, {k.dtype}, {v.dtype}")
     dt = _DTYPES[q.dtype]
     es = q.element_size()
     q, k, v = _as_bthd(q, "q", es), _as_bthd(k, "k", es), _as_bthd(v, "v", es)
@@ -108,7 +108,7 @@ def bwd_raw(q, k, v, r, w, causal, eps, y, hnorm, bits, dy, key_padding_mask=Non
     dropout_p / seed must be the forward's."""
     L = _native.lib()
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise TypeError(f"q/k/v must share dtype float32 or bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+        raise TypeError(f"q/k/v must share dtype float32, bfloat16 or float16, got {q.dtype}, {k.dtype}, {v.dtype}")
     dt = _DTYPES[q.dtype]
     es = q.element_size()
     q, k, v = _as_bthd(q, "q", es), _as_bthd(k, "k", es), _as_bthd(v, "v", es)
@@ -163,11 +163,6 @@ class ScreeningCoreFunction(torch.autograd.Function):
 def screening_core(q, k, v, r, w, causal=True, eps=1e-8, key_padding_mask=None, dropout_p=0.0, seed=0):
     """Fused screening attention core; see the module docstring.  dropout_p > 0
     applies attention dropout (attention.py:190) with the keep mask of `seed`."""
-    if q.dtype == torch.float16:
-        # no fp16 kernels: compute in fp32 and return fp16
-        out = ScreeningCoreFunction.apply(q.float(), k.float(), v.float(), r, w, causal, eps, key_padding_mask,
-                                          dropout_p, seed)
-        return out.to(torch.float16)
     return ScreeningCoreFunction.apply(q, k, v, r, w, causal, eps, key_padding_mask, dropout_p, seed)
 
 
@@ -175,7 +170,7 @@ def _decode_args(q, kcache, vcache, r, w):
     if not q.is_cuda:
         raise RuntimeError("decode_step runs on the GPU only (got a CPU tensor)")
     if q.dtype not in _DTYPES or kcache.dtype != q.dtype or vcache.dtype != q.dtype:
-        raise TypeError(f"decode_step needs q and the caches in one of float32 / bfloat16, got "
+        raise TypeError(f"decode_step needs q and the caches in one of float32 / bfloat16 / float16, got "
                         f"{q.dtype}, {kcache.dtype}, {vcache.dtype}")
     B, H, D = q.shape
     if q.stride(2) != 1:

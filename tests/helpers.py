@@ -9,16 +9,72 @@ import torch
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-def rel_err(got, ref):
-    """max|got-ref| / max|ref|  (per tensor; alpha is mostly zero, so elementwise
-    relative error is meaningless)."""
+# Slices of a tensor checked at their own scale by rel_err: per (b, h) for
+# the (B, T, H, D) layout of q/k/v/y and their gradients; for other tensors
+# per index of the axes the caller names (e.g. heads=(0, 1) for (B, H, T) row
+# norms or (B, H, D) decode rows).  A slice is measured against
+# max(max|ref over the slice|, SLICE_FLOOR * max|ref|): a head whose values
+# reach a hundredth of the largest head's is held to the tolerance on its own
+# magnitude, and a smaller one at that hundredth.  Below it the comparison
+# would divide by values that rounding alone decides: pairs within bf16
+# rounding of the threshold (alpha <= (r 2^-9)^2, about 1.6e-5) are voted on
+# K^ rounded to bf16, and an fp32 head output that cancels to far below its
+# terms carries their rounding.
+SLICE_FLOOR = 1e-2
+
+
+def errors(got, ref, heads=None):
+    """Error metrics of got against ref (float64):
+      max    max|got-ref| / max|ref| over the whole tensor (alpha is mostly
+             zero, so elementwise relative error is meaningless);
+      fro    ||got-ref|| / ||ref|| (Frobenius);
+      slice  the largest per-slice max|got-ref| / max(max|ref slice|,
+             SLICE_FLOOR max|ref|), slices as described above (= max when
+             the tensor has no head axes).
+    A reference of all zeros gives the absolute error for each."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
-    scale = np.max(np.abs(ref))
-    diff = np.max(np.abs(got - ref)) if got.size else 0.0
+    d = np.abs(got - ref)
+    scale = float(np.max(np.abs(ref))) if ref.size else 0.0
+    dmax = float(np.max(d)) if d.size else 0.0
     if scale == 0.0:
-        return float(diff)
-    return float(diff / scale)
+        return {"max": dmax, "fro": dmax, "slice": dmax}
+    out = {"max": dmax / scale,
+           "fro": float(np.sqrt(np.sum(d * d)) / np.sqrt(np.sum(ref * ref)))}
+    if heads is None and ref.ndim == 4:
+        heads = (0, 2)
+    if heads:
+        axes = tuple(a for a in range(ref.ndim) if a not in heads)
+        sref = np.max(np.abs(ref), axis=axes)
+        sd = np.max(d, axis=axes)
+        out["slice"] = float(np.max(sd / np.maximum(sref, SLICE_FLOOR * scale)))
+    else:
+        out["slice"] = out["max"]
+    return out
+
+
+def rel_err(got, ref, heads=None):
+    """The largest of errors(got, ref, heads): whole-tensor max-relative,
+    Frobenius ratio and per-head max-relative, so an error cannot hide behind
+    a larger head of the same tensor."""
+    return max(errors(got, ref, heads).values())
+
+
+def head_sum_err(got, ref, abs_sum):
+    """Per-entry error of per-head sums (dr, dw): max over heads of
+    |got_h - ref_h| / (sum over the head's pairs of |term|).  A sum of terms
+    of both signs can cancel to far below its terms, and its rounding error
+    scales with the terms, not with the total; for a sum of terms of one sign
+    this is the plain relative error.  Heads with no terms must be exactly
+    zero."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    abs_sum = np.asarray(abs_sum, dtype=np.float64)
+    d = np.abs(got - ref)
+    if np.any((abs_sum == 0) & (d != 0)):
+        return float("inf")
+    nz = abs_sum > 0
+    return float(np.max(d[nz] / abs_sum[nz])) if np.any(nz) else 0.0
 
 
 def qkv(B, Tq, Tk, H, D, seed=0, dtype=torch.float32):

@@ -128,12 +128,11 @@ class TestMultiscreenLM:
         assert torch.equal(got, ids)
 
 
-def test_float16_model_keeps_a_float32_cache():
-    # the kernels compute in float32 or bfloat16: a float16 model's KV cache is
-    # float32 (decode casts its query to the cache dtype and back)
+def test_float16_model_keeps_a_float16_cache():
+    # the kernels take float16 directly (MSA_F16): the cache keeps the model's dtype
     from multiscreen.attention import KVCache
     c = KVCache(2, 8, 4, 16, torch.float16, "cpu")
-    assert c.k.dtype == torch.float32 and c.v.shape == (2, 8, 4, 16)
+    assert c.k.dtype == torch.float16 and c.v.shape == (2, 8, 4, 16)
 
 
 def test_lm_matches_reference_golden():
@@ -202,13 +201,50 @@ def test_fused_qkv_projection_matches_separate_linears():
     assert m.q_proj.weight.grad is None or m.q_proj.weight.grad.abs().sum() == 0
 
 
-def test_fused_weight_cache_follows_in_place_updates():
+def test_stacked_projection_follows_weight_updates_of_every_kind():
+    """In place, through .data (no version bump), and by reassignment: the
+    next no-grad forward sees the new weights."""
     from multiscreen import ScreeningAttention
     torch.manual_seed(1)
     m = ScreeningAttention(32, 2)
     x = torch.randn(1, 4, 32)
+    mem = torch.randn(1, 6, 32)
     with torch.no_grad():
         a = m.project_qkv(x, x, x)[2].clone()
-        m.v_proj.weight.mul_(2.0)           # in place: bumps the version counter
-        b = m.project_qkv(x, x, x)[2]
-    torch.testing.assert_close(b, 2.0 * a, rtol=1e-6, atol=1e-6)
+        m.v_proj.weight.mul_(2.0)
+        torch.testing.assert_close(m.project_qkv(x, x, x)[2], 2.0 * a, rtol=1e-6, atol=1e-6)
+        m.v_proj.weight.data.mul_(3.0)      # .data: the version counter does not move
+        torch.testing.assert_close(m.project_qkv(x, x, x)[2], 6.0 * a, rtol=1e-6, atol=1e-6)
+        kv0 = m.project_qkv(x, mem, mem)[1].clone()
+        m.k_proj.weight.data.copy_(-m.k_proj.weight.data)
+        torch.testing.assert_close(m.project_qkv(x, mem, mem)[1], -kv0, rtol=1e-6, atol=1e-6)
+        m.s_r.fill_(-3.0)                   # r = 1.05: most pairs are live
+        y0 = m(x, x, x)
+        assert y0.abs().max() > 0
+        m.q_proj.weight.data.add_(torch.randn_like(m.q_proj.weight))
+        assert not torch.equal(m(x, x, x), y0)
+
+
+def test_projection_hooks_are_honoured():
+    """A forward hook on a projection (weight_norm, LoRA-style wrappers) takes
+    the per-module calls, so the hook runs and its result is used."""
+    from multiscreen import ScreeningAttention
+    torch.manual_seed(2)
+    m = ScreeningAttention(32, 2)
+    x = torch.randn(1, 5, 32)
+    mem = torch.randn(1, 7, 32)
+    calls = []
+
+    def hook(mod, inp, out):
+        calls.append(mod)
+        return out * 2.0
+
+    want = m.project(x, m.k_proj) * 2.0
+    h = m.k_proj.register_forward_hook(hook)
+    got = m.project_qkv(x, x, x)[1]
+    torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-6)
+    got = m.project_qkv(x, mem, mem)[1]
+    torch.testing.assert_close(got, m.project(mem, m.k_proj), rtol=1e-6, atol=1e-6)
+    assert len(calls) >= 2
+    h.remove()
+    torch.testing.assert_close(m.project_qkv(x, x, x)[1], want / 2.0, rtol=1e-6, atol=1e-6)

@@ -32,7 +32,7 @@ def test_library_loads_and_exports_header():
 
 def test_version_and_sizes():
     L = _native.lib()
-    assert L.msa_version() == (0 << 16) | (1 << 8)
+    assert L.msa_version() == (0 << 16) | (3 << 8)
     # B=4, T=8192, H=8, D=64 bf16: one normalised K^ copy, then the screen's
     # work-plan table: 32 lanes x kmax entries of 32 bytes.  The size serves a
     # causal or a non-causal call: kmax = 68 causal (4 heads per XCD x 68
@@ -46,7 +46,9 @@ def test_version_and_sizes():
     assert L.msa_tile_bits_words(1, 1, 64, 1100) == 2 * 2
     # D=16 is padded to 32 in the workspace; one head, one item per lane at most
     assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4 + 1024
-    # backward workspace: (dr, dw) partial per (b, h, 32-key unit), then dh
+    # fp16 takes bf16's sizes (2-byte elements)
+    assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 2) == one + 32 * 128 * 32
+    # backward workspace: (dr, dw) partial per (b, h, 32-query unit), then dh
     # (b, h, Tq_pad, DP) in the input type and 1/|q| (b, h, Tq_pad) fp32, each
     # 256-byte aligned
     assert L.msa_bwd_workspace_bytes(4, 8, 8192, 8192, 64, 1) == \
@@ -69,7 +71,7 @@ def _fwd(L, **kw):
 
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(D=48), 1, "head_dim"),
-    (dict(dtype=2), 1, "dtype"),
+    (dict(dtype=3), 1, "dtype"),
     (dict(q=None), 1, "q is null"),
     (dict(q=24), 1, "aligned"),
     (dict(qs=(1024, 60, 8)), 1, "strides"),

@@ -13,11 +13,11 @@ from helpers import correlated_qkv, np64, rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 5e-3}
 DEV = "cuda"
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("D", [32, 128])
 def test_decode_head_dims(D, dtype):
     from multiscreen import ops
@@ -35,4 +35,4 @@ def test_decode_head_dims(D, dtype):
         assert torch.equal(single, split), L
         ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, np.array(r), np.array(w))
         assert np.max(np.abs(ref)) > 0
-        assert rel_err(np64(split), ref) <= TOL[dtype], L
+        assert rel_err(np64(split), ref, heads=(0, 1)) <= TOL[dtype], L

@@ -1,8 +1,10 @@
 """Parity of the HIP path (libmsa.so, through its C ABI) with the CPU oracle.
 
-Tolerances: max|got-ref|/max|ref| per tensor <= 1e-5 in
-fp32 and <= 2e-2 in bf16, for outputs and all gradients.  The bf16 oracle is
-the float64 oracle on the same bf16-rounded inputs.
+Tolerances: <= 1e-5 in fp32 and <= 2e-2 in bf16, for
+outputs and all gradients, on each of max|got-ref|/max|ref| per tensor, the
+Frobenius ratio ||got-ref||/||ref|| and the per-(b, h) max-relative error
+(helpers.rel_err); float16 is held to 5e-3.  The bf16 and fp16 oracle is the
+float64 oracle on the same rounded inputs.
 """
 
 import math
@@ -17,7 +19,7 @@ from helpers import (GOLDEN_ATTENTION, correlated_qkv, golden_inputs, golden_mod
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 5e-3}
 DEV = "cuda"
 
 
@@ -92,7 +94,7 @@ def _case_inputs(case, dtype, seed=0):
     return q, k, v, kpm
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("case", FWD_CASES, ids=[f"c{i}" for i in range(len(FWD_CASES))])
 def test_forward_parity(case, dtype):
     B, Tq, Tk, H, D, causal, r, w, use_kpm = case
@@ -104,10 +106,10 @@ def test_forward_parity(case, dtype):
     assert np.max(np.abs(yref)) > 1e-3, "vacuous case"
     assert rel_err(np64(y), yref) <= TOL[dtype]
     nref = np.linalg.norm(href, axis=-1)
-    assert rel_err(hnorm.cpu().double().numpy(), nref) <= TOL[dtype]
+    assert rel_err(hnorm.cpu().double().numpy(), nref, heads=(0, 1)) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("case", FWD_CASES, ids=[f"c{i}" for i in range(len(FWD_CASES))])
 def test_backward_parity(case, dtype):
     B, Tq, Tk, H, D, causal, r, w, use_kpm = case
@@ -136,7 +138,7 @@ def test_backward_parity(case, dtype):
 # Attention dropout (attention.py:190): the kernels and the oracle share the
 # counter-based keep mask of include/msa.h, so they agree to the usual
 # tolerances; cases 1-3 cover ragged T, key padding and Tq != Tk.
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("ci", [0, 1, 2, 3])
 def test_dropout_parity(ci, dtype):
     case = FWD_CASES[ci]
@@ -306,7 +308,7 @@ def test_window_and_threshold_skip_are_exact():
     assert torch.equal(y0[:, 7 * 64:8 * 64], y1[:, 7 * 64:8 * 64])
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 def test_decode_matches_forward_rows(dtype):
     B, T, H, D = 3, 700, 4, 64
     q, k, v = correlated_qkv(B, T, T, H, D, seed=6, dtype=dtype, rho=0.35)
@@ -318,7 +320,7 @@ def test_decode_matches_forward_rows(dtype):
     for L in (1, 2, 64, 257, 700):
         y = ops.decode_step(q[:, L - 1].to(DEV), kc, vc, L, rg, wg)
         torch.cuda.synchronize()
-        assert rel_err(np64(y), yfull[:, L - 1]) <= TOL[dtype], L
+        assert rel_err(np64(y), yfull[:, L - 1], heads=(0, 1)) <= TOL[dtype], L
 
 
 def test_decode_window_hint_changes_only_the_grid():
@@ -339,7 +341,7 @@ def test_decode_window_hint_changes_only_the_grid():
         for hint in (1, 2048, math.ceil(max(w)), 10 ** 6):
             assert torch.equal(ops.decode_step(qd, kc, vc, L, rg, wg, window_hint=hint), base), (L, hint)
         ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, np.array(r), np.array(w))
-        assert rel_err(np64(base), ref) <= 2e-2, L
+        assert rel_err(np64(base), ref, heads=(0, 1)) <= 2e-2, L
 
 
 @pytest.mark.parametrize("name", GOLDEN_ATTENTION)
@@ -385,7 +387,7 @@ def test_cfg2_full_size_sampled_rows_bf16():
 
 
 def test_float16_model_generate():
-    # a float16 model (model.half()) decodes through float32 caches; its greedy
+    # a float16 model (model.half()) decodes through float16 caches; its greedy
     # tokens are those of re-running forward() on the prefix
     from multiscreen import MultiscreenLM
     torch.manual_seed(0)
