@@ -240,8 +240,10 @@ struct HeadParams {
   float w;     // window w_h > 1
   float iw;    // 1/w
   int wc;      // ceil(w) (capped at 2^30): for integer distance d, d < w  <=>  d < wc
-  float thr;   // 1 - 1/r - 1e-6: s > thr for every pair with 1 - r(1-s) > 0 (a
-               // conservative gate; the exact test follows wherever it passes)
+  float thr;   // 1 - 1/r - 1e-5: s > thr for every pair with 1 - r(1-s) > 0 when
+               // s is formed from exact products with fp32 accumulation and
+               // fp32 1/|x| (error below (D+3) 2^-24 <= 8e-6 for D <= 128): a
+               // conservative gate; the exact test follows wherever it passes
   int wsh;     // window as one unsigned compare: dd in window  <=>
   unsigned wlim;  // (unsigned)(dd + wsh) < wlim
 };
@@ -259,7 +261,7 @@ __device__ inline HeadParams head_params_rw(float r, float w, bool causal) {
   p.iw = 1.0f / p.w;
   const float c = ceilf(p.w);
   p.wc = !(c > 0.0f) ? 0 : (c > 1073741824.0f ? 1073741824 : (int)c);
-  p.thr = 1.0f - 1.0f / p.r - 1e-6f;
+  p.thr = 1.0f - 1.0f / p.r - 1e-5f;
   p.wsh = causal ? 0 : p.wc - 1;
   p.wlim = p.wc == 0 ? 0u : (causal ? (unsigned)p.wc : (unsigned)(2 * p.wc - 1));
   return p;
@@ -315,6 +317,12 @@ __device__ inline float softmask_dw(int dd, float iw) {
   const float rel = (float)(-dd);
   const float x = rel * iw;
   return 0.5f * sinpif(x) * 3.14159265358979f * rel * iw * iw;
+}
+
+// max(x[l], x[l ^ 32]) in every lane (as half_sum, with max).
+__device__ inline float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
 }
 
 // x[l] + x[l ^ 32] in every lane, with one v_permlane32_swap (no LDS): the

@@ -21,6 +21,8 @@
 //                   1/|v_j| folded into P.  The epilogue applies TanhNorm
 //                   (norm.py:23-25) and writes y in (B,T,H,D) and |h| per row.
 //                   No T x T matrix is ever materialised.
+#include <type_traits>
+
 #include "msa_device.h"
 #include "msa_internal.h"
 
@@ -287,6 +289,44 @@ size_t screen_plan_bytes(const Geometry& g) {
   return round_up((int64_t)32 * kmax * (int64_t)sizeof(ScreenItem), 256);
 }
 
+// ---------------------------------------------------------------------------
+// Screen operands.  The screen votes on S^T = K^ Q^T with K^ = k/|k| stored
+// in a 2-byte type for 2-byte inputs, so each vote sees s up to the rounding
+// of K^: |s_screen - s| <= u sum_d |q^_d k^_d| <= u (unit roundoff u, unit
+// vectors).  The live-unit bitmap must hold every pair with alpha > 0 (the
+// live and backward passes visit nothing else, and a missed pair's gradient
+// terms are linear in a = 1 - r(1-s)), so the vote's gate is lowered by that
+// bound.  Both inputs of 2-byte types screen in fp16, not bf16: u = 2^-12
+// instead of 2^-9, at the same MFMA rate, so the lowered gate admits about
+// 1% more 32x32 units instead of about 10% (measured on the configs[1]
+// inputs).  The operands are power-of-two scaled into fp16's normal range,
+// which keeps their values exact up to that rounding: K^ times 2^10 (its
+// components are at most 1, and down to 2^-24 stay normal), each raw query
+// row times the 2^e that puts its largest component in [2^10, 2^11) (bf16
+// has 8 significant bits, so every component above 2^-24 of the largest is
+// exact in fp16).  fp32 inputs screen in fp32 (u = 2^-24 per K^ component).
+// The vote's gate, in s, is 1 - 1/r - kScreenSlack, the slack covering the
+// rounding above, fp32 accumulation of D <= 128 products ((D+3) 2^-24) and
+// the fp32 1/|q| and 1/|k|.
+// ---------------------------------------------------------------------------
+template <typename T>
+using ScreenOp = typename std::conditional<sizeof(T) == 2, f16, float>::type;
+template <typename T>
+constexpr float kKhatScale = sizeof(T) == 2 ? 1024.0f : 1.0f;
+template <typename T>
+constexpr float kScreenSlack = sizeof(T) == 2 ? 2.441406e-4f + 1e-5f : 1e-5f;  // 2^-12 + 1e-5
+
+// Power of two p with max|x| * p in [2^10, 2^11) (1 for a zero or non-finite
+// max): scales a query row into fp16's normal range exactly.
+__device__ inline float row_pow2(float mx) {
+  if (!(mx > 0.0f) || !(mx < INFINITY)) return 1.0f;
+  int ex;
+  (void)frexpf(mx, &ex);  // mx = m 2^ex, m in [0.5, 1)
+  int e = 11 - ex;
+  e = e > 126 ? 126 : (e < -126 ? -126 : e);
+  return ldexpf(1.0f, e);
+}
+
 // 16-byte chunk per thread per row; a key row of DP elements spans CPR
 // threads, and a thread covers kPrepRows rows RPB apart (all loads first).
 constexpr int kPrepRows = 4;
@@ -321,10 +361,10 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
     for (int e = 0; e < VEC; ++e) ss += x[u][e] * x[u][e];
 #pragma unroll
     for (int o = 1; o < CPR; o <<= 1) ss += __shfl_xor(ss, o);
-    float inv = 1.0f / fmaxf(sqrtf(ss), a.eps);
+    float inv = kKhatScale<T> / fmaxf(sqrtf(ss), a.eps);
     if (t >= a.Tk || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + t])) inv = 0.0f;
     if (t < a.Tk_pad) {
-      T* p = (T*)a.khat + ((int64_t)bh * a.Tk_pad + t) * DP + d0;
+      ScreenOp<T>* p = (ScreenOp<T>*)a.khat + ((int64_t)bh * a.Tk_pad + t) * DP + d0;
 #pragma unroll
       for (int e = 0; e < VEC; e += 4)
         store4(p + e, x[u][e] * inv, x[u][e + 1] * inv, x[u][e + 2] * inv, x[u][e + 3] * inv);
@@ -403,9 +443,10 @@ __device__ inline int ceil_tiles(int x) { return -floor_tiles(-x); }
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void fwd_screen_kernel(FwdKArgs a) {
-  using M = Mma<T>;
+  using S = ScreenOp<T>;  // operand type of the screen's MFMAs
+  using M = Mma<S>;
   using frag = typename M::frag;
-  using G = ScreenTile<T, DP>;
+  using G = ScreenTile<S, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NS = G::NS;
   __shared__ __attribute__((aligned(16))) char ring[NS * G::TILEB];
 
@@ -504,12 +545,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   auto half_mma = [&](const char* slot, int kh, f32x16 (&acc)[2]) {
     frag kf[NKS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) kf[ks] = M::load((const T*)(slot + aoff[kh][ks]));
+    for (int ks = 0; ks < NKS; ++ks) kf[ks] = M::load((const S*)(slot + aoff[kh][ks]));
 #pragma unroll
     for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[qh][r] = 0.0f;
-    if constexpr (sizeof(T) == 2) {
+    if constexpr (sizeof(S) == 2) {
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
@@ -523,10 +564,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   };
   // Threshold vote on key half kh of the tile at k0: a(s) is monotone in s and
-  // s = acc/|q_i|, so a 32x32 unit has a live pair iff its largest in-window
-  // acc exceeds (1 - 1/r)|q_i|.  The vote compares with qthr (the head's
-  // conservative gate times |q_i|), so a unit within 1e-6 below the threshold
-  // may be marked too; the live pass's exact test gives its pairs alpha = 0.
+  // s = acc/(|q_i| c_i) (c_i: the operands' power-of-two scales), so a 32x32
+  // unit has a live pair iff its largest in-window acc exceeds
+  // (1 - 1/r)|q_i| c_i.  The vote compares with qthr, that threshold lowered
+  // by kScreenSlack, so every unit with a live pair is marked, and a unit
+  // whose pairs all lie within the slack below the threshold may be marked
+  // too; the live pass's exact test gives those pairs alpha = 0.
   // The compare's lane mask is the wave's vote, so the result is
   // wave-uniform: bit qh set iff unit (qh, kh) has a passing pair.  Register r
   // of the half holds key k0 + 32kh + 16(r/8) + 8half + r%8.  Tiles wholly
@@ -594,13 +637,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int n_fast0 = fa <= fb - 1 ? ohi - (fb - 1) : nsteps;  // steps [n_fast0, n_fast1)
   const int n_fast1 = fa <= fb - 1 ? ohi - fa + 1 : nsteps;
 
-  // s = acc/max(|q|, eps) passes the gate iff acc > thr max(|q|, eps); a gate
-  // at or below 0 (r at most 1 + 1e-6) is taken as 0, the exact threshold of r = 1
+  // s = acc/(max(|q|, eps) c) passes the lowered gate iff
+  // acc > (1 - 1/r - slack) max(|q|, eps) c, with c = kKhatScale times the
+  // row's power of two (a negative gate, r within the slack of 1, marks every
+  // unit with a pair above it: still a superset of the live units)
+  {
+    const float vthr = 1.0f - 1.0f / hp.r - kScreenSlack<T>;
 #pragma unroll
-  for (int qh = 0; qh < 2; ++qh) {
-    qthr[qh] = fmaxf(hp.thr, 0.0f) / qrow[qh].inv_norm(a.eps);
+    for (int qh = 0; qh < 2; ++qh) {
+      float mx = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qf[qh * NKS + ks] = qrow[qh].f[ks];
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) mx = fmaxf(mx, fabsf(Mma<T>::get(qrow[qh].f[ks], e)));
+      const float c = sizeof(S) == 2 ? row_pow2(half_max(mx)) : 1.0f;
+      qthr[qh] = vthr / qrow[qh].inv_norm(a.eps) * (c * kKhatScale<T>);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        if constexpr (sizeof(S) == 2) {  // bf16 or fp16 rows, scaled by c into fp16
+          f32x16 t;
+#pragma unroll
+          for (int e = 0; e < PER; ++e) t[e] = Mma<T>::get(qrow[qh].f[ks], e) * c;
+          qf[qh * NKS + ks] = M::pack(t, 0);
+        } else {
+          qf[qh * NKS + ks] = qrow[qh].f[ks];
+        }
+      }
+    }
   }
 
   {

@@ -60,12 +60,15 @@ def rel_err(got, ref, heads=None):
     return max(errors(got, ref, heads).values())
 
 
-def head_sum_err(got, ref, abs_sum):
+def head_sum_err(got, ref, abs_sum, floor=SLICE_FLOOR):
     """Per-entry error of per-head sums (dr, dw): max over heads of
-    |got_h - ref_h| / (sum over the head's pairs of |term|).  A sum of terms
-    of both signs can cancel to far below its terms, and its rounding error
-    scales with the terms, not with the total; for a sum of terms of one sign
-    this is the plain relative error.  Heads with no terms must be exactly
+    |got_h - ref_h| / max(S_h, floor * max_h S_h), S_h the sum over the head's
+    pairs of |term|.  A sum of terms of both signs can cancel to far below its
+    terms, and its rounding error scales with the terms, not with the total;
+    for a sum of terms of one sign this is the plain relative error.  As for
+    slices, a head whose terms weigh less than `floor` of the heaviest head's
+    is held to that level (its few terms sit near the threshold, where a's
+    relative error r|ds|/a is large).  Heads with no terms must be exactly
     zero."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
@@ -74,7 +77,10 @@ def head_sum_err(got, ref, abs_sum):
     if np.any((abs_sum == 0) & (d != 0)):
         return float("inf")
     nz = abs_sum > 0
-    return float(np.max(d[nz] / abs_sum[nz])) if np.any(nz) else 0.0
+    if not np.any(nz):
+        return 0.0
+    scale = np.maximum(abs_sum, floor * np.max(abs_sum))
+    return float(np.max(d[nz] / scale[nz]))
 
 
 def qkv(B, Tq, Tk, H, D, seed=0, dtype=torch.float32):

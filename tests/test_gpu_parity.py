@@ -231,12 +231,16 @@ def test_backward_deterministic():
     (1, 2048, 8, [1.1, 1.2, 1.3, 1.4, 1.5, 1.6, 1.8, 2.0], [1e5, 3000.0, 1700.0, 900.0, 2048.0, 64.0, 1e5, 500.0]),
 ], ids=["bh4", "bh8", "bh72", "t2048"])
 def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
+    # fp32: the bitmap holds every unit with a live pair, and beyond those only
+    # units with a pair within the vote's slack (1e-5 in s) below the threshold
     D = 64
     q, k, v = correlated_qkv(B, T, T, H, D, seed=4, dtype=torch.float32, rho=0.3)
     y, hnorm, bits = _run_fwd(q, k, v, r, w, True)
     # the bitmap is kept per 32x32 unit: 2*nqt rows of ceil(2*nkt/32) words
-    nW, nA, act = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True, tile=32)
-    _, nA64, act64 = O.tile_counts(np64(q), np64(k), np.array(r), np.array(w), True, tile=64)
+    rr = np.array(r)
+    nW, nA, act = O.tile_counts(np64(q), np64(k), rr, np.array(w), True, tile=32)
+    _, _, band = O.tile_counts(np64(q), np64(k), 1.0 / (1.0 / rr + SLACK_F32), np.array(w), True, tile=32)
+    _, nA64, act64 = O.tile_counts(np64(q), np64(k), rr, np.array(w), True, tile=64)
     nqu = nku = T // 32
     words = (nku + 31) // 32
     b = bits.cpu().numpy().view(np.uint32).reshape(B, H, nqu, words)
@@ -244,53 +248,80 @@ def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
     for ku in range(nku):
         got[..., ku] = (b[..., ku // 32] >> (ku % 32)) & 1
     assert nA > 0
-    assert np.array_equal(got, act)
-    # a 64x64 tile is live iff one of its four units is
-    assert np.array_equal(got.reshape(B, H, nqu // 2, 2, nku // 2, 2).any(axis=(3, 5)), act64)
+    assert np.all(got[act]), "a unit with a live pair is not marked"
+    assert not np.any(got & ~band), "a marked unit has no pair within the slack"
+    # a 64x64 tile is marked iff one of its four units is
+    got64 = got.reshape(B, H, nqu // 2, 2, nku // 2, 2).any(axis=(3, 5))
+    assert np.all(got64[act64])
 
 
-def _bf16_unit_bits(q, k, r, w, causal):
-    """Live 32x32 units of the bf16 screen's exact test, restated in float64:
-    s = (q . k^)/|q| with k^ = bf16(k/|k|) as the forward stores it, and the
-    distance of each unit's best in-window pair from the threshold."""
-    qn = np64(q) / np.maximum(np.linalg.norm(np64(q), axis=-1, keepdims=True), 1e-8)
+# The vote's slack below the threshold 1 - 1/r, in s (kScreenSlack in
+# msa_fwd.hip): fp32 screens on fp32 K^; bf16 and fp16 screen on fp16 K^
+# (unit roundoff 2^-12), plus fp32 accumulation.
+SLACK_F32 = 1e-5
+SLACK_16 = 2.0 ** -12 + 1e-5
+
+
+def _fp16_screen_units(q, k, r, w, causal):
+    """The 2-byte screen's vote restated in float64 on its own operands:
+    K^ = fp16(1024 k/|k|) as prep_k stores it, each raw query row scaled by
+    the power of two c that puts its largest component in [2^10, 2^11) and
+    rounded to fp16, s_screen = (q16 . K^) / (1024 c max(|q|, eps)).  Returns
+    the units whose best in-window s_screen exceeds 1 - 1/r - SLACK_16, the
+    distance of that best value from the vote threshold, and the units with
+    an exact live pair (s from the rounded inputs in float64)."""
+    q64, k64 = np64(q), np64(k)
+    qnorm = np.maximum(np.linalg.norm(q64, axis=-1, keepdims=True), 1e-8)
+    mx = np.max(np.abs(q64), axis=-1, keepdims=True)
+    ex = np.frexp(np.where(mx > 0, mx, 1.0))[1]
+    c = np.where(mx > 0, np.ldexp(1.0, 11 - ex), 1.0)
+    q16 = (q64 * c).astype(np.float16).astype(np.float64)
     kf = k.float()
-    kh = (kf / kf.norm(dim=-1, keepdim=True).clamp_min(1e-8)).bfloat16().double().numpy()
-    B, T, H, _ = qn.shape
+    kh = (1024.0 * kf / kf.norm(dim=-1, keepdim=True).clamp_min(1e-8)).half().double().numpy()
+    qn = q64 / qnorm
+    kn = k64 / np.maximum(np.linalg.norm(k64, axis=-1, keepdims=True), 1e-8)
+    B, T, H, _ = q64.shape
     n = T // 32
-    live = np.zeros((B, H, n, n), dtype=bool)
+    vote = np.zeros((B, H, n, n), dtype=bool)
+    exact = np.zeros((B, H, n, n), dtype=bool)
     margin = np.full((B, H, n, n), np.inf)
     i = np.arange(T)[:, None]
     j = np.arange(T)[None, :]
     for h in range(H):
-        s = np.einsum("bid,bjd->bij", qn[:, :, h], kh[:, :, h])
+        s_scr = np.einsum("bid,bjd->bij", q16[:, :, h], kh[:, :, h]) / (1024.0 * c[:, :, h] * qnorm[:, :, h])
+        s_ex = np.einsum("bid,bjd->bij", qn[:, :, h], kn[:, :, h])
         wc = math.ceil(w[h])
         inside = ((i - j >= 0) & (i - j < wc)) if causal else (np.abs(i - j) < wc)
         thr = 1.0 - 1.0 / r[h]
-        d = np.where(inside[None], s - thr, -np.inf).reshape(B, n, 32, n, 32)
+        d = np.where(inside[None], s_scr - (thr - SLACK_16), -np.inf).reshape(B, n, 32, n, 32)
         best = d.max(axis=(2, 4))
-        live[:, h] = best > 0
+        vote[:, h] = best > 0
         margin[:, h] = np.abs(best)
-    return live, margin
+        e = np.where(inside[None], s_ex - thr, -np.inf).reshape(B, n, 32, n, 32)
+        exact[:, h] = e.max(axis=(2, 4)) > 0
+    return vote, margin, exact
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("r", [1.9, 2.0, 2.1, 1.5])
-def test_bf16_bitmap_matches_exact_test(r):
-    # the bf16 screen's bitmap is the exact test on its own operands (bf16 K^,
-    # raw q scaled by 1/|q|), restated in float64; units within 1e-5 of the
-    # threshold excepted
+def test_2byte_bitmap_matches_exact_test(r, dtype):
+    # the 2-byte screen's bitmap is its vote on its own operands (fp16 K^,
+    # scaled fp16 q), restated in float64, units within 1e-5 of the vote's
+    # threshold excepted (fp32 accumulation); and it holds every unit with
+    # an exactly live pair (no pair with alpha > 0 is ever missed)
     B, T, H, D = 2, 1024, 4, 64
-    q, k, v = qkv(B, T, T, H, D, seed=11, dtype=torch.bfloat16)
+    q, k, v = qkv(B, T, T, H, D, seed=11, dtype=dtype)
     rr, ww = [r] * H, [100.0, 400.0, 700.0, 1e5]
     y, hnorm, bits = _run_fwd(q, k, v, rr, ww, True)
-    want, margin = _bf16_unit_bits(q, k, rr, ww, True)
+    want, margin, exact = _fp16_screen_units(q, k, rr, ww, True)
     n = T // 32
     words = (n + 31) // 32
     b = bits.cpu().numpy().view(np.uint32).reshape(B, H, n, words)
     got = np.zeros((B, H, n, n), dtype=bool)
     for ku in range(n):
         got[..., ku] = (b[..., ku // 32] >> (ku % 32)) & 1
-    assert want.sum() > 0
+    assert exact.sum() > 0
+    assert np.all(got[exact]), int((exact & ~got).sum())
     diff = got != want
     assert np.all(margin[diff] < 1e-5), (int(diff.sum()), float(margin[diff].min()) if diff.any() else 0.0)
 
