@@ -178,6 +178,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k| (0 if padded or masked) of the unit's key rows
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v|
+  __shared__ float mt[64], mdt[64];  // soft-mask and dm/dw tables of the current unit (unit_mask_table)
   __shared__ typename Mma<T>::frag qh[2 * (DP / Mma<T>::KS)][kWave];  // own raw q, dh operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
@@ -320,6 +321,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
       const float iv = inv_len(s2v, a.eps);
       wave_lds_sync();
       if (half == 0) { sk[m] = ik; sv[m] = iv; }
+      unit_mask_table<true>(mt, mdt, qu * kUnit - k0 - 31, hp, lane);
       wave_lds_sync();
     }
     // scaled in place: s = (q . k)/|k|, dp = dH . v^
@@ -332,25 +334,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
     }
-    // a conservative gate on the products (s > thr |q|), then the exact
-    // test only for registers where some lane passes
-    const int rel0 = i - (k0 + 8 * half);
+    // a conservative gate on the products (s > thr |q|) picks the
+    // registers where some lane may pass; there every lane forms its pair's
+    // terms branch-free (a = 0 below the threshold, the mask and dm/dw, 0
+    // outside the window, from the unit's tables: entry
+    // l32 - 8half + 31 - 16(r/8) - r%8 for register r)
     {
+      const float* mrow = mt + (l32 - 8 * half + 8);  // entry 23 - (16(r/8) + r%8): a constant offset
+      const float* drow = mdt + (l32 - 8 * half + 8);
+      // (rows past Tq hold q = 0, so s = 0 and a = 1 - r <= 0: no term)
       const uint32_t pm0 = pass_mask(s, thq);
-      for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
-        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
+      for_each_set<false>(pm0, [&](int r) {
+        const int off = 16 * (r >> 3) + (r & 7);
         const float sv = s[r] * iql;
-        const float av = trim(sv, hp.r);
-        float ds = 0.0f;
-        if (av > 0.0f && valid && in_window(dd, hp)) {
-          const float c = a.drop.on ? dropout_factor(a.drop, bh, i, i - dd) : 1.0f;
-          const float mk = softmask(dd, hp.iw) * c;
-          const float g = dp[r];
-          ds = 2.0f * av * hp.r * mk * g;
-          dr_acc -= 2.0f * av * (1.0f - sv) * mk * g;
-          dw_acc += av * av * g * softmask_dw(dd, hp.iw) * c;
-        }
-        dp[r] = ds;
+        const float av = fmaxf(trim(sv, hp.r), 0.0f);
+        float g = dp[r];
+        if (a.drop.on) g *= dropout_factor(a.drop, bh, i, k0 + 8 * half + off);
+        const float t = 2.0f * av * mrow[23 - off] * g;
+        dr_acc -= t * (1.0f - sv);
+        dw_acc += av * av * g * drow[23 - off];
+        dp[r] = hp.r * t;
       });
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -430,6 +433,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
   using frag = typename M::frag;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   __shared__ __attribute__((aligned(16))) float sq[32];  // 1/|q| of the current query unit's rows
+  __shared__ float mt[64];  // soft-mask table of the current unit (unit_mask_table)
   __shared__ typename Mma<T>::frag kvs[2 * (DP / Mma<T>::KS)][kWave];  // own raw k, v operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int ku, bh;
@@ -559,6 +563,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     zero_tail(qf);
     wave_lds_sync();
     if (half == 0) sq[l32] = iqv;
+    unit_mask_table<false>(mt, nullptr, q0 - k0 - 31, hp, lane);
     wave_lds_sync();
     // register r -> query q0 + rowof(r, half), lane -> key j.  Scaled in
     // place: s = (q . k)/|q|, dp = (dh . v)/|v|.
@@ -587,25 +592,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
         dp[r] *= ivl;
       }
     }
-    // a conservative gate on the products (s > thr |k|), then the exact
-    // test only for registers where some lane passes
-    const int rel0 = (q0 + 8 * half) - j;
+    // a conservative gate on the products (s > thr |k|) picks the
+    // registers where some lane may pass; there every lane forms its pair's
+    // weight and ds branch-free (the mask, 0 outside the window, from the
+    // unit's table: entry 16(r/8) + r%8 + 8half - l32 + 31 for register r)
     {
+      const float* mrow = mt + (8 * half - l32 + 31);
       const uint32_t pm0 = pass_mask(s, thk);
-      for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
-        const int dd = rel0 + 16 * (r >> 3) + (r & 7);
-        const float sv = s[r] * ikl;
-        const float av = trim(sv, hp.r);
-        float p = 0.0f, ds = 0.0f;
-        if (av > 0.0f && in_window(dd, hp)) {
-          const float c = a.drop.on ? dropout_factor(a.drop, bh, j + dd, j) : 1.0f;
-          const float mk = softmask(dd, hp.iw) * c;
-          const float g = dp[r];
-          p = av * av * mk;
-          ds = 2.0f * av * hp.r * mk * g;
-        }
-        s[r] = p;
-        dp[r] = ds;
+      for_each_set<false>(pm0, [&](int r) {
+        const int off = 16 * (r >> 3) + (r & 7);
+        const float av = fmaxf(trim(s[r] * ikl, hp.r), 0.0f);
+        float mk = mrow[off];
+        if (a.drop.on) mk *= dropout_factor(a.drop, bh, q0 + 8 * half + off, j);
+        const float am = av * mk;
+        s[r] = av * am;
+        dp[r] = 2.0f * hp.r * am * dp[r];
       });
 #pragma unroll
       for (int r = 0; r < 16; ++r)

@@ -300,8 +300,76 @@ __device__ inline void for_each_set(uint32_t pm, Fn&& fn) {
   }
 }
 
+// cos(pi x) and sin(pi x) for |x| <= 1 (x clamped there), branch-free and
+// without a library call: with y = |x| and t = min(y, 1 - y) in [0, 1/2],
+// cos(pi y) = +-cos(pi t) (minus for y > 1/2) and sin(pi y) = sin(pi t); the
+// Taylor series of cos(pi t) and sin(pi t) to t^12 and t^13 are within
+// 6.4e-9 and 6.7e-10 of them on [0, 1/2] (next terms pi^14 t^14/14! and
+// pi^15 t^15/15!), below fp32 rounding.  Coefficients (-1)^k pi^2k/(2k)!
+// and (-1)^k pi^(2k+1)/(2k+1)!, evaluated by Horner's rule in t^2.
+__device__ inline float cospi_poly(float u) {  // u = t^2
+  float c = 0.001929574309403922f;
+  c = fmaf(c, u, -0.02580689139001405f);
+  c = fmaf(c, u, 0.23533063035889312f);
+  c = fmaf(c, u, -1.3352627688545893f);
+  c = fmaf(c, u, 4.058712126416768f);
+  c = fmaf(c, u, -4.934802200544679f);
+  return fmaf(c, u, 1.0f);
+}
+__device__ inline float sinpi_poly(float t, float u) {  // u = t^2
+  float c = 0.00046630280576761234f;
+  c = fmaf(c, u, -0.007370430945714348f);
+  c = fmaf(c, u, 0.08214588661112819f);
+  c = fmaf(c, u, -0.5992645293207919f);
+  c = fmaf(c, u, 2.550164039877345f);
+  c = fmaf(c, u, -5.167712780049969f);
+  c = fmaf(c, u, 3.141592653589793f);
+  return c * t;
+}
+// Soft mask m = (cos(pi dd/w) + 1)/2 (attention.py:114) for an in-window
+// distance (|dd| < w, so |dd/w| < 1); out of the window the value is finite
+// and the caller masks it.
+__device__ inline float mask_fast(int dd, float iw) {
+  const float y = fminf(fabsf((float)dd * iw), 1.0f);
+  const float t = fminf(y, 1.0f - y);
+  const float c = cospi_poly(t * t);
+  return 0.5f + 0.5f * (y > 0.5f ? -c : c);
+}
+// The same mask and dm/dw = (pi/2) dd sin(pi dd/w) / w^2 (the w-derivative
+// of (cos(pi (j-i)/w) + 1)/2, attention.py:114).
+__device__ inline void mask_fast_dw(int dd, float iw, float& m, float& dm) {
+  const float x = fminf(fmaxf((float)dd * iw, -1.0f), 1.0f);
+  const float y = fabsf(x);
+  const float t = fminf(y, 1.0f - y);
+  const float u = t * t;
+  const float c = cospi_poly(u);
+  m = 0.5f + 0.5f * (y > 0.5f ? -c : c);
+  const float sn = copysignf(sinpi_poly(t, u), x);
+  dm = (0.5f * 3.14159265358979f) * (float)dd * sn * iw * iw;
+}
+
 // Branch-free in-window test on the integer distance dd = i - j.
 __device__ inline bool in_window(int dd, const HeadParams& hp) { return (unsigned)(dd + hp.wsh) < hp.wlim; }
+
+// Soft-mask table of one 32x32 unit (queries q0.., keys k0..): its pairs'
+// distances dd = i - j span dmin .. dmin + 62 with dmin = q0 - k0 - 31, so
+// lane l (l < 63) evaluates entry l = the mask of distance dmin + l, 0
+// outside the window (and, with `dw`, dm/dw in a second table).  A pair
+// then reads its mask instead of evaluating it.  Written by one wave for its
+// own use: the caller syncs (wave_lds_sync) before reading.
+template <bool kDw>
+__device__ inline void unit_mask_table(float* mt, float* mdt, int dmin, const HeadParams& hp, int lane) {
+  const int dd = dmin + lane;
+  const bool in = lane < 63 && in_window(dd, hp);
+  if constexpr (kDw) {
+    float m, dm;
+    mask_fast_dw(dd, hp.iw, m, dm);
+    mt[lane] = in ? m : 0.0f;
+    mdt[lane] = in ? dm : 0.0f;
+  } else {
+    mt[lane] = in ? mask_fast(dd, hp.iw) : 0.0f;
+  }
+}
 
 // Trim-and-square pre-square value a = 1 - r (1 - s)  (attention.py:90).
 __device__ inline float trim(float s, float r) { return 1.0f - r * (1.0f - s); }

@@ -754,6 +754,7 @@ void fwd_live_kernel(FwdKArgs a) {
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k_j| (0 if padded or masked) of the current unit
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
+  __shared__ float mt[64];  // soft-mask table of the current unit (unit_mask_table)
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
   float head_r, head_w;
@@ -895,6 +896,7 @@ void fwd_live_kernel(FwdKArgs a) {
         sv[m] = iv;
         sk[m] = ik;
       }
+      unit_mask_table<false>(mt, nullptr, qu * kUnit - k0 - 31, hp, lane);
       wave_lds_sync();
     }
     {
@@ -926,22 +928,28 @@ void fwd_live_kernel(FwdKArgs a) {
     guard_frags(vc);
     guard_frags(id);
     load_v(nl, vc);
-    // P^T[j][i] = alpha_ij m_ij / |v_j|: a conservative gate on the raw
-    // products (s > thr), the exact test only where some lane passes
-    const int rel0 = i - (k0 + 8 * half);
+    // P^T[j][i] = alpha_ij m_ij / |v_j|: a conservative gate on the products
+    // (s > thr) picks the registers where some lane may pass; there every
+    // lane forms its pair's weight branch-free (alpha = 0 below the
+    // threshold, the mask, 0 outside the window, from the unit's table:
+    // register r holds distance i - k0 - 8half - 16(r/8) - r%8, entry
+    // l32 - 8half + 31 - 16(r/8) - r%8)
     {
+      const float* mrow = mt + (l32 - 8 * half + 8);  // entry 23 - (16(r/8) + r%8): a constant offset
       const uint32_t pm0 = pass_mask(s, thq);
-      for_each_set<sizeof(T) == 2>(pm0, [&](int r) {
-        const int dd = rel0 - (16 * (r >> 3) + (r & 7));
-        const float av = trim(s[r] * iq, hp.r);
-        float p = 0.0f;
-        if (av > 0.0f && in_window(dd, hp)) {
-          p = av * av * softmask(dd, hp.iw);
-          if constexpr (!kScaleRowsNotWeights<T>) p *= sv[rowof(r, half)];
-          if (a.drop.on) p *= dropout_factor(a.drop, bh, i, i - dd);
-        }
+      for_each_set<false>(pm0, [&](int r) {
+        const int off = 16 * (r >> 3) + (r & 7);
+        const float av = fmaxf(trim(s[r] * iq, hp.r), 0.0f);
+        float p = av * av * mrow[23 - off];
+        if (a.drop.on) p *= dropout_factor(a.drop, bh, i, k0 + 8 * half + off);
         s[r] = p;
       });
+      if constexpr (!kScaleRowsNotWeights<T>) {
+        float vsc[16];
+        read_row_scales(sv, half, vsc);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] *= vsc[r];
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (((pm0 >> r) & 1u) == 0u) s[r] = 0.0f;
