@@ -178,7 +178,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
   __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k| (0 if padded or masked) of the unit's key rows
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v|
-  __shared__ float mt[64], mdt[64];  // soft-mask and dm/dw tables of the current unit (unit_mask_table)
+  __shared__ float mtab[128];  // soft-mask table of the current unit, then its dm/dw table (unit_mask_table)
   __shared__ typename Mma<T>::frag qh[2 * (DP / Mma<T>::KS)][kWave];  // own raw q, dh operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
@@ -286,6 +286,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
 
   for (;;) {
     const int k0 = cur * kUnit;
+    // the unit's mask tables first, while few values are live (the LDS sync
+    // after the products below covers these writes too; this iteration's
+    // writes follow the previous one's reads in the wave's LDS order)
+    unit_mask_table<true>(mtab, mtab + 64, qu * kUnit - k0 - 31, hp, lane);
     const int nxt = walk.next();
     zero_tail(kc);
     zero_tail(vc);
@@ -321,7 +325,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
       const float iv = inv_len(s2v, a.eps);
       wave_lds_sync();
       if (half == 0) { sk[m] = ik; sv[m] = iv; }
-      unit_mask_table<true>(mt, mdt, qu * kUnit - k0 - 31, hp, lane);
       wave_lds_sync();
     }
     // scaled in place: s = (q . k)/|k|, dp = dH . v^
@@ -340,8 +343,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
     // outside the window, from the unit's tables: entry
     // l32 - 8half + 31 - 16(r/8) - r%8 for register r)
     {
-      const float* mrow = mt + (l32 - 8 * half + 8);  // entry 23 - (16(r/8) + r%8): a constant offset
-      const float* drow = mdt + (l32 - 8 * half + 8);
+      // entry 23 - (16(r/8) + r%8) of each table: constant offsets from one base
+      const float* mrow = mtab + (l32 - 8 * half + 8);
       // (rows past Tq hold q = 0, so s = 0 and a = 1 - r <= 0: no term)
       const uint32_t pm0 = pass_mask(s, thq);
       for_each_set<false>(pm0, [&](int r) {
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
         if (a.drop.on) g *= dropout_factor(a.drop, bh, i, k0 + 8 * half + off);
         const float t = 2.0f * av * mrow[23 - off] * g;
         dr_acc -= t * (1.0f - sv);
-        dw_acc += av * av * g * drow[23 - off];
+        dw_acc += av * av * g * mrow[64 + 23 - off];
         dp[r] = hp.r * t;
       });
 #pragma unroll
