@@ -57,7 +57,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=300)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
-    p.add_argument("--no-configs", action="store_true", help="skip the configs[2..4] legs")
+    p.add_argument("--no-configs", action="store_true", help="skip the supplementary legs")
+    p.add_argument("--legs", default="", help="comma-separated supplementary legs to run (default: all)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--calib-copy", action="store_true",
                    help="end with one elementwise pass over 2 GiB (rocprofv3 --pmc byte-counter calibration)")
@@ -569,7 +570,10 @@ def main():
                 ("cfg2_trained_regime", lambda: trained_regime_bench(L, ops, torch)),
                 ("cfg2_f16", lambda: fp16_bench(L, ops, torch, q, k, v, dy, r, w)),
                 ("ref_fused_module_fwd", lambda: ref_module_bench(torch)))
+        only = set(x for x in args.legs.split(",") if x)
         for key, leg in legs:
+            if only and key not in only:
+                continue
             try:
                 extra[key] = leg()
             except Exception as e:  # reported in the line, not hidden

@@ -79,24 +79,6 @@ template <> struct Vec16<float> {
   __device__ static inline float get(const type& a, int e) { return a[e]; }
 };
 
-// Sum over aligned groups of G lanes (G a power of two <= 64), every lane of
-// a group getting the group's total: DPP lane swaps within rows of 16 (xor 1,
-// xor 2, then the 8- and 16-lane mirrors, which pair each half with the other
-// once both halves hold their own sums), lane shuffles beyond.
-template <int G>
-__device__ inline float group_sum(float x) {
-  auto dpp = [](float v, auto ctrl) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xf, 0xf, false));
-  };
-  if constexpr (G >= 2) x += dpp(x, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
-  if constexpr (G >= 4) x += dpp(x, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
-  if constexpr (G >= 8) x += dpp(x, std::integral_constant<int, 0x141>{});  // row_half_mirror
-  if constexpr (G >= 16) x += dpp(x, std::integral_constant<int, 0x140>{}); // row_mirror
-#pragma unroll
-  for (int o = 16; o < G; o <<= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
 // First key of head h's window at position pos, and its number of chunks.
 __device__ inline int64_t window_lo(const DecArgs& a, int h) {
   const HeadParams hp = head_params(a.r, a.w, h, true);

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace msa {
 
 typedef __bf16 bf16;
@@ -402,6 +404,24 @@ __device__ inline float half_sum(float x) {
   return __int_as_float(r[0]) + __int_as_float(r[1]);
 }
 
+// Sum over aligned groups of G lanes (G a power of two <= 64), every lane of
+// a group getting the group's total: DPP lane swaps within rows of 16 (xor 1,
+// xor 2, then the 8- and 16-lane mirrors, which pair each half with the other
+// once both halves hold their own sums), lane shuffles beyond.
+template <int G>
+__device__ inline float group_sum(float x) {
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (G >= 2) x += dpp(x, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) x += dpp(x, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) x += dpp(x, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (G >= 16) x += dpp(x, std::integral_constant<int, 0x140>{}); // row_mirror
+#pragma unroll
+  for (int o = 16; o < G; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -477,6 +497,23 @@ __device__ inline void store_creg_row(T* row, int D, int half, Fn fn) {
         if (d < D) row[d] = fn(dblk, r);
       }
   }
+}
+
+// Loads one 16-byte chunk (8 bf16/fp16 or 4 fp32 values) as fp32.
+__device__ inline void load_chunk(const bf16* p, float (&x)[8]) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (float)v[e];
+}
+__device__ inline void load_chunk(const f16* p, float (&x)[8]) {
+  const f16x8 v = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (float)v[e];
+}
+__device__ inline void load_chunk(const float* p, float (&x)[4]) {
+  const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = v[e];
 }
 
 // Loads 4 consecutive values as fp32.

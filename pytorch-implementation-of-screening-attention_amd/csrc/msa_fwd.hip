@@ -346,11 +346,11 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
   for (int u = 0; u < kPrepRows; ++u) {
     const int64_t t = ((int64_t)blockIdx.x * kPrepRows + u) * RPB + threadIdx.x / CPR;
     const bool valid = t < a.Tk && d0 < a.D;
+    // one 16-byte load per row chunk (rows past Tk read row 0, then zeroed)
+    load_chunk((const T*)a.k + b * a.ks.sb + (valid ? t : 0) * a.ks.st + h * a.ks.sh + (d0 < a.D ? d0 : 0), x[u]);
+    if (!valid) {
 #pragma unroll
-    for (int e = 0; e < VEC; e += 4) {
-      f32x4 v4 = {0.f, 0.f, 0.f, 0.f};
-      if (valid) v4 = load4((const T*)a.k + b * a.ks.sb + t * a.ks.st + h * a.ks.sh + d0 + e);
-      x[u][e] = v4[0]; x[u][e + 1] = v4[1]; x[u][e + 2] = v4[2]; x[u][e + 3] = v4[3];
+      for (int e = 0; e < VEC; ++e) x[u][e] = 0.0f;
     }
   }
 #pragma unroll
@@ -359,8 +359,7 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss += x[u][e] * x[u][e];
-#pragma unroll
-    for (int o = 1; o < CPR; o <<= 1) ss += __shfl_xor(ss, o);
+    ss = group_sum<CPR>(ss);  // the row's CPR lanes
     float inv = kKhatScale<T> / fmaxf(sqrtf(ss), a.eps);
     if (t >= a.Tk || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + t])) inv = 0.0f;
     if (t < a.Tk_pad) {
