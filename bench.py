@@ -488,8 +488,11 @@ def ref_module_bench(torch, reps=20):
     fp32 on x ~ N(0,1) of shape (4, T, 512), s_r = -2 (r = 1.135), default
     windows; latency (median of `reps` event-timed calls after warm-up) and
     torch.cuda.max_memory_allocated for the forward (eval, no_grad) and for
-    forward + backward (train)."""
+    forward + backward (train).  The reference measures in a process of its
+    own; here the other legs' tensors are resident, so their bytes (allocated
+    before this leg starts) are subtracted from each peak."""
     from multiscreen import ScreeningAttention
+    held = torch.cuda.memory_allocated()
     torch.manual_seed(0)
     m = ScreeningAttention(512, num_heads=8, causal=True).cuda()
     with torch.no_grad():
@@ -513,13 +516,13 @@ def ref_module_bench(torch, reps=20):
             torch.cuda.reset_peak_memory_stats()
             m(x, x, x)
             torch.cuda.synchronize()
-            mem_fwd = torch.cuda.max_memory_allocated() / 1e6
+            mem_fwd = (torch.cuda.max_memory_allocated() - held) / 1e6
         m.train()
         xg = x.clone().requires_grad_()
         torch.cuda.reset_peak_memory_stats()
         m(xg, xg, xg).sum().backward()
         torch.cuda.synchronize()
-        mem_fb = torch.cuda.max_memory_allocated() / 1e6
+        mem_fb = (torch.cuda.max_memory_allocated() - held) / 1e6
         m.zero_grad(set_to_none=True)
         ms = sorted(times)[len(times) // 2]
         row = {"T": T, "fwd_ms": round(ms, 4), "fwd_peak_mb": round(mem_fwd, 1), "fwd_bwd_peak_mb": round(mem_fb, 1),
@@ -532,6 +535,7 @@ def ref_module_bench(torch, reps=20):
     return {"workload": "reference benchmarks/bench_triton.py: ScreeningAttention(512, 8, causal) module forward, "
                         "fp32, B=4, s_r=-2 (r=1.135), default windows",
             "ref_hardware": "RTX 4060 Ti (BENCHMARK_REPORT_TRITON.md:61-85; a different GPU)",
+            "peak_mb_note": f"max_memory_allocated minus the {held / 1e6:.1f} MB the other legs hold",
             "rows": rows}
 
 

@@ -347,7 +347,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
       const float* mrow = mtab + (l32 - 8 * half + 8);
       // (rows past Tq hold q = 0, so s = 0 and a = 1 - r <= 0: no term)
       const uint32_t pm0 = pass_mask(s, thq);
-      for_each_set<false>(pm0, [&](int r) {
+      for_each_set(pm0, [&](int r) {
         const int off = 16 * (r >> 3) + (r & 7);
         const float sv = s[r] * iql;
         const float av = fmaxf(trim(sv, hp.r), 0.0f);
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
     {
       const float* mrow = mt + (8 * half - l32 + 31);
       const uint32_t pm0 = pass_mask(s, thk);
-      for_each_set<false>(pm0, [&](int r) {
+      for_each_set(pm0, [&](int r) {
         const int off = 16 * (r >> 3) + (r & 7);
         const float av = fmaxf(trim(s[r] * ikl, hp.r), 0.0f);
         float mk = mrow[off];

@@ -936,7 +936,7 @@ void fwd_live_kernel(FwdKArgs a) {
     {
       const float* mrow = mt + (l32 - 8 * half + 8);  // entry 23 - (16(r/8) + r%8): a constant offset
       const uint32_t pm0 = pass_mask(s, thq);
-      for_each_set<false>(pm0, [&](int r) {
+      for_each_set(pm0, [&](int r) {
         const int off = 16 * (r >> 3) + (r & 7);
         const float av = fmaxf(trim(s[r] * iq, hp.r), 0.0f);
         float p = av * av * mrow[23 - off];
