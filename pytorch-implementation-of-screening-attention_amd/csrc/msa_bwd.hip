@@ -337,17 +337,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] *= sc[r];
     }
-    // a conservative gate on the products (s > thr |q|) picks the
-    // registers where some lane may pass; there every lane forms its pair's
-    // terms branch-free (a = 0 below the threshold, the mask and dm/dw, 0
-    // outside the window, from the unit's tables: entry
-    // l32 - 8half + 31 - 16(r/8) - r%8 for register r)
+    // every lane forms its pair's terms branch-free (a = 0 below the
+    // threshold, the mask and dm/dw, 0 outside the window, from the unit's
+    // tables: entry l32 - 8half + 31 - 16(r/8) - r%8 for register r), for
+    // every register; with dropout, only for the registers where some lane
+    // may pass a conservative gate on the products (s > thr |q|), so the
+    // pair hash runs there only
     {
       // entry 23 - (16(r/8) + r%8) of each table: constant offsets from one base
       const float* mrow = mtab + (l32 - 8 * half + 8);
       // (rows past Tq hold q = 0, so s = 0 and a = 1 - r <= 0: no term)
-      const uint32_t pm0 = pass_mask(s, thq);
-      for_each_set(pm0, [&](int r) {
+      auto body = [&](int r) {
         const int off = 16 * (r >> 3) + (r & 7);
         const float sv = s[r] * iql;
         const float av = fmaxf(trim(sv, hp.r), 0.0f);
@@ -357,10 +357,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
         dr_acc -= t * (1.0f - sv);
         dw_acc += av * av * g * mrow[64 + 23 - off];
         dp[r] = hp.r * t;
-      });
+      };
+      if (a.drop.on) {  // the pair's hash only where some lane may pass
+        const uint32_t pm0 = pass_mask(s, thq);
+        for_each_set(pm0, body);
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (((pm0 >> r) & 1u) == 0u) dp[r] = 0.0f;
+        for (int r = 0; r < 16; ++r)
+          if (((pm0 >> r) & 1u) == 0u) dp[r] = 0.0f;
+      } else {  // every register: a = 0 gives no term, and no mask or branches
+#pragma unroll
+        for (int r = 0; r < 16; ++r) body(r);
+      }
     }
     // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
     // the key rows, one 32-column block of d at a time
@@ -595,14 +602,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
         dp[r] *= ivl;
       }
     }
-    // a conservative gate on the products (s > thr |k|) picks the
-    // registers where some lane may pass; there every lane forms its pair's
-    // weight and ds branch-free (the mask, 0 outside the window, from the
-    // unit's table: entry 16(r/8) + r%8 + 8half - l32 + 31 for register r)
+    // every lane forms its pair's weight and ds branch-free (the mask, 0
+    // outside the window, from the unit's table: entry 16(r/8) + r%8 + 8half
+    // - l32 + 31 for register r), for every register; with dropout, only for
+    // the registers where some lane may pass a conservative gate on the
+    // products (s > thr |k|), so the pair hash runs there only
     {
       const float* mrow = mt + (8 * half - l32 + 31);
-      const uint32_t pm0 = pass_mask(s, thk);
-      for_each_set(pm0, [&](int r) {
+      auto body = [&](int r) {
         const int off = 16 * (r >> 3) + (r & 7);
         const float av = fmaxf(trim(s[r] * ikl, hp.r), 0.0f);
         float mk = mrow[off];
@@ -610,10 +617,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
         const float am = av * mk;
         s[r] = av * am;
         dp[r] = 2.0f * hp.r * am * dp[r];
-      });
+      };
+      if (a.drop.on) {  // the pair's hash only where some lane may pass
+        const uint32_t pm0 = pass_mask(s, thk);
+        for_each_set(pm0, body);
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (((pm0 >> r) & 1u) == 0u) { s[r] = 0.0f; dp[r] = 0.0f; }
+        for (int r = 0; r < 16; ++r)
+          if (((pm0 >> r) & 1u) == 0u) { s[r] = 0.0f; dp[r] = 0.0f; }
+      } else {  // every register: a = 0 gives no term, and no mask or branches
+#pragma unroll
+        for (int r = 0; r < 16; ++r) body(r);
+      }
     }
     // ds/|q| (fp16: the Q^T rows take 1/|q| instead, below)
     float qsc[16];
