@@ -754,6 +754,7 @@ void fwd_live_kernel(FwdKArgs a) {
   __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k_j| (0 if padded or masked) of the current unit
   __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
   __shared__ float mt[64];  // soft-mask table of the current unit (unit_mask_table)
+  __shared__ frag qsh[NKS][kWave];  // own raw q operand fragments
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
   int qu, bh;
   float head_r, head_w;
@@ -823,9 +824,9 @@ void fwd_live_kernel(FwdKArgs a) {
         if (KS * ks >= a.D) f[ks] = M::zero();
     }
   };
-  // own queries as raw B operands (lane -> query) and 1/|q_i|; their loads go
-  // first, the first unit's behind them
-  frag qf[NKS];
+  // own queries as raw B operands (lane -> query), kept in LDS and read back
+  // per unit (the registers go to the unit rows), and 1/|q_i|; their loads
+  // go first, the first unit's behind them
   float iq;
   frag kc[NKS], vc[NKS];
   bool kok;
@@ -837,7 +838,7 @@ void fwd_live_kernel(FwdKArgs a) {
     kok = key_ok(cur);
     iq = qr.inv_norm(a.eps);
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qf[ks] = qr.f[ks];
+    for (int ks = 0; ks < NKS; ++ks) qsh[ks][lane] = qr.f[ks];
   }
   const float thq = hp.thr / iq;  // s > thr  <=>  (k . q)/|k| > thr |q|
   f32x16 o[NDH];
@@ -856,18 +857,24 @@ void fwd_live_kernel(FwdKArgs a) {
     float s2k = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-    if constexpr (sizeof(T) == 2) {
+    {
+      frag qf[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        s = M::mma_ng(kc[ks], qf[ks], s);
-        s2k = frag_dot(kc[ks], kc[ks], s2k);
-      }
-      guard_frags(kc);
-    } else {
+      for (int ks = 0; ks < NKS; ++ks) qf[ks] = qsh[ks][lane];
+      if constexpr (sizeof(T) == 2) {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        s = M::mma(kc[ks], qf[ks], s);
-        s2k = frag_dot(kc[ks], kc[ks], s2k);
+        for (int ks = 0; ks < NKS; ++ks) {
+          s = M::mma_ng(kc[ks], qf[ks], s);
+          s2k = frag_dot(kc[ks], kc[ks], s2k);
+        }
+        guard_frags(kc);
+        guard_frags(qf);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          s = M::mma(kc[ks], qf[ks], s);
+          s2k = frag_dot(kc[ks], kc[ks], s2k);
+        }
       }
     }
     // each operand's registers take the next unit's rows as soon as they are
@@ -927,31 +934,38 @@ void fwd_live_kernel(FwdKArgs a) {
     guard_frags(vc);
     guard_frags(id);
     load_v(nl, vc);
-    // P^T[j][i] = alpha_ij m_ij / |v_j|: a conservative gate on the products
-    // (s > thr) picks the registers where some lane may pass; there every
-    // lane forms its pair's weight branch-free (alpha = 0 below the
-    // threshold, the mask, 0 outside the window, from the unit's table:
-    // register r holds distance i - k0 - 8half - 16(r/8) - r%8, entry
-    // l32 - 8half + 31 - 16(r/8) - r%8)
+    // P^T[j][i] = alpha_ij m_ij / |v_j|: every lane forms its pair's weight
+    // branch-free (alpha = 0 below the threshold, the mask, 0 outside the
+    // window, from the unit's table: register r holds distance i - k0 - 8half
+    // - 16(r/8) - r%8, entry l32 - 8half + 31 - 16(r/8) - r%8), for every
+    // register; with dropout, only for the registers where some lane may pass
+    // a conservative gate on the products (s > thr), so the pair hash runs
+    // there only
     {
       const float* mrow = mt + (l32 - 8 * half + 8);  // entry 23 - (16(r/8) + r%8): a constant offset
-      const uint32_t pm0 = pass_mask(s, thq);
-      for_each_set(pm0, [&](int r) {
+      auto body = [&](int r) {
         const int off = 16 * (r >> 3) + (r & 7);
         const float av = fmaxf(trim(s[r] * iq, hp.r), 0.0f);
         float p = av * av * mrow[23 - off];
         if (a.drop.on) p *= dropout_factor(a.drop, bh, i, k0 + 8 * half + off);
         s[r] = p;
-      });
+      };
+      if (a.drop.on) {
+        const uint32_t pm0 = pass_mask(s, thq);
+        for_each_set(pm0, body);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (((pm0 >> r) & 1u) == 0u) s[r] = 0.0f;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) body(r);
+      }
       if constexpr (!kScaleRowsNotWeights<T>) {
         float vsc[16];
         read_row_scales(sv, half, vsc);
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] *= vsc[r];
       }
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (((pm0 >> r) & 1u) == 0u) s[r] = 0.0f;
     }
     // H^T[d][i] += sum_j V^T[d][j] P^T[j][i]
     frag pb[NC];
@@ -966,7 +980,6 @@ void fwd_live_kernel(FwdKArgs a) {
     if (nxt < 0) break;
     cur = nxt;
   }
-  guard_frags(qf);
 
   // TanhNorm per query row (lane -> query, registers -> d), y in (B,T,H,D)
   float ss = 0.0f;
