@@ -889,6 +889,7 @@ void fwd_live_kernel(FwdKArgs a) {
     // 1/|k_j| and 1/|v_j| of the lane's key row, to LDS (read back in
     // register order), then V^T by identity MFMA
     vzero(vc);
+    float ivl;  // this lane's 1/|v| (its row m)
     {
       float s2v = 0.0f;
 #pragma unroll
@@ -896,6 +897,7 @@ void fwd_live_kernel(FwdKArgs a) {
       s2v = half_sum(s2v);
       s2k = half_sum(s2k);
       const float iv = inv_len(s2v, a.eps);
+      ivl = iv;
       const float ik = kok_c ? inv_len(s2k, a.eps) : 0.0f;
       wave_lds_sync();
       if (half == 0) {
@@ -915,8 +917,15 @@ void fwd_live_kernel(FwdKArgs a) {
     frag id[NC];  // formed per unit: fewer registers held across the loop
 #pragma unroll
     for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
-    float vsc[16];  // fp16: 1/|v_j| of the transposed rows (register order)
-    if constexpr (kScaleRowsNotWeights<T>) read_row_scales(sv, half, vsc);
+    // fp16: each lane's V row takes its 1/|v| before the transposes (in fp32,
+    // rounded once to fp16: the value the transposed row would get), which
+    // holds one scale per lane instead of sixteen
+    if constexpr (kScaleRowsNotWeights<T>) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) vc[ks][e] = (T)((float)vc[ks][e] * ivl);
+    }
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk) {
       f32x16 tr;
@@ -924,10 +933,6 @@ void fwd_live_kernel(FwdKArgs a) {
       for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) tr = M::mma_ng(vc[dblk * NC + c], id[c], tr);
-      if constexpr (kScaleRowsNotWeights<T>) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tr[r] *= vsc[r];
-      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) ta[dblk * NC + c] = M::pack(tr, c * PER);
     }
