@@ -43,8 +43,10 @@ namespace msa {
 //   per-XCD mode (B*H >= 32): heads are dealt to XCDs widest window first in
 //     boustrophedon order and stay there (a head's K^ stays in one L2); each
 //     XCD's items are dealt over its 4 engine lanes;
-//   global mode (fewer heads, where one XCD per head would leave XCDs idle or
-//     overloaded): all items are dealt over all 32 lanes.
+//   group mode (fewer heads, where one XCD per head would leave XCDs idle or
+//     overloaded): XCD x takes groups x, x+8, ... of every head, and deals
+//     them over its 4 engine lanes.
+// Either way each XCD's plan is made by one planner block of its own.
 // Screen block p takes entry (p % 8, (p >> 3) % 4, p >> 5) of the table;
 // positions past a lane's items hold bh = -1 (the block exits at once).
 // Which items run where changes only the time, never the bitmap (live bits
@@ -60,7 +62,7 @@ struct ScreenPlan {
   ScreenItem* table;  // [8 XCDs][4 engine lanes][kmax]
   int kmax;           // positions per lane
   int seg;            // steps (tile offsets) per item at most (<= 256)
-  int per_xcd;        // 1: per-XCD mode, 0: global mode
+  int per_xcd;        // 1: per-XCD mode, 0: group mode
 };
 
 struct PrepKArgs {
@@ -143,17 +145,19 @@ __host__ __device__ inline bool group_offsets(int Tq, int Tk, int nqt, int wc, b
 }
 
 // Visits the planned items: fn(bh, grp, olo, ohi) for each (head slot, group)
-// pair's near-equal cut of its offset range into ceil(steps / seg) items.
-// heads[slot] and the integer windows wcs[slot] are in LDS for the first
-// kPlanMaxHeads slots; beyond them (per-XCD mode without ranking only) slot
-// jh is head 8*jh + x.
+// pair's near-equal cut of its offset range into ceil(steps / seg) items, over
+// groups g0, g0 + gstep, ...  heads[slot] and the integer windows wcs[slot]
+// are in LDS for the first kPlanMaxHeads slots; beyond them (per-XCD mode
+// without ranking only) slot jh is head 8*jh + x.
 template <typename Fn>
-__device__ inline void plan_items(const PrepKArgs& a, int x, const int* heads, const int* wcs, int nh, Fn&& fn) {
+__device__ inline void plan_items(const PrepKArgs& a, int x, const int* heads, const int* wcs, int nh, int g0,
+                                  int gstep, Fn&& fn) {
   const int ngroups = (a.nqt + 3) / 4;
+  const int ng = ngroups > g0 ? (ngroups - g0 + gstep - 1) / gstep : 0;  // groups visited per head
   const bool causal = a.causal != 0;
   const int seg = a.plan.seg;
-  for (int idx = threadIdx.x; idx < nh * ngroups; idx += blockDim.x) {
-    const int slot = idx / ngroups, grp = idx - slot * ngroups;
+  for (int idx = threadIdx.x; idx < nh * ng; idx += blockDim.x) {
+    const int slot = idx / ng, grp = g0 + (idx - slot * ng) * gstep;
     const bool cached = slot < kPlanMaxHeads;
     const int bh = cached ? heads[slot] : 8 * slot + x;
     const int wc = cached ? wcs[slot] : plan_wc(a.w[bh % a.H]);
@@ -177,9 +181,9 @@ __device__ inline void plan_deal(int i, int nl, int& e, int& j) {
   e = (j & 1) ? nl - 1 - r : r;
 }
 
-// Planner block x (256 threads).  Per-XCD mode: block x writes the 4 lanes
-// of XCD x.  Global mode: block 0 writes all 32 lanes (lane L = XCD L % 8,
-// engine L / 8).
+// Planner block x (256 threads) writes the 4 lanes of XCD x: in per-XCD mode
+// from the heads dealt to it, in group mode from groups x, x+8, ... of every
+// head.
 __device__ void screen_plan(const PrepKArgs& a, int x) {
   __shared__ int heads[kPlanMaxHeads], wcs[kPlanMaxHeads];
   __shared__ float keys[kPlanMaxRanked], rh[kPlanMaxRanked], wh[kPlanMaxRanked];
@@ -187,11 +191,11 @@ __device__ void screen_plan(const PrepKArgs& a, int x) {
   __shared__ int hist[257], start[257];
   __shared__ int total;
   const bool per_xcd = a.plan.per_xcd != 0;
-  if (!per_xcd && x != 0) return;
-  const int t = threadIdx.x, nl = per_xcd ? 4 : 32, kmax = a.plan.kmax;
+  const int t = threadIdx.x, nl = 4, kmax = a.plan.kmax;
+  const int g0 = per_xcd ? 0 : x, gstep = per_xcd ? 1 : 8;
   for (int i = t; i < 257; i += blockDim.x) hist[i] = 0;
   const int BH = a.B * a.H;
-  const int nh = per_xcd ? xcd_head_count(BH, x) : BH;  // global mode: BH < 32
+  const int nh = per_xcd ? xcd_head_count(BH, x) : BH;  // group mode: BH < 32
   // the one global read of the windows (the planner runs beside prep_k's
   // stream, where every dependent memory round trip is slow)
   const bool small_h = a.H <= kPlanMaxRanked;
@@ -217,7 +221,7 @@ __device__ void screen_plan(const PrepKArgs& a, int x) {
   __syncthreads();
   // items by length (at most seg <= 256), longest first; the order among
   // items of one length is whatever the atomics give (it only moves time)
-  plan_items(a, x, heads, wcs, nh, [&](int, int, int lo, int hi) { atomicAdd(&hist[hi - lo + 1], 1); });
+  plan_items(a, x, heads, wcs, nh, g0, gstep, [&](int, int, int lo, int hi) { atomicAdd(&hist[hi - lo + 1], 1); });
   __syncthreads();
   if (t < 64) {  // exclusive prefix over lengths 256 .. 1: lane t holds 256-4t .. 253-4t
     int v[4], sum = 0;
@@ -241,12 +245,9 @@ __device__ void screen_plan(const PrepKArgs& a, int x) {
     if (t == 63) total = incl;
   }
   __syncthreads();
-  // lane e of this planner -> table lane (XCD, engine)
-  auto lane_base = [&](int e) -> ScreenItem* {
-    const int xcd = per_xcd ? x : e % 8, eng = per_xcd ? e : e / 8;
-    return a.plan.table + (xcd * 4 + eng) * kmax;
-  };
-  plan_items(a, x, heads, wcs, nh, [&](int bh, int grp, int lo, int hi) {
+  // lane e of this planner -> table lane (XCD x, engine e)
+  auto lane_base = [&](int e) -> ScreenItem* { return a.plan.table + (x * 4 + e) * kmax; };
+  plan_items(a, x, heads, wcs, nh, g0, gstep, [&](int bh, int grp, int lo, int hi) {
     const int pos = atomicAdd(&start[hi - lo + 1], 1);
     int e, j;
     plan_deal(pos, nl, e, j);
@@ -270,17 +271,25 @@ void screen_plan_dims(const Geometry& g, int& seg, int& kmax, int& per_xcd) {
   seg = (5 * g.nkt + 15) / 16;
   seg = seg < 8 ? 8 : (seg > 256 ? 256 : seg);
   const int64_t BH = (int64_t)g.B * g.H;
-  // global mode for few heads; per-XCD mode keeps at most kPlanMaxHeads per XCD
+  // group mode for few heads; per-XCD mode keeps at most kPlanMaxHeads per XCD
   per_xcd = BH >= 32 ? 1 : 0;
   const int ngroups = (g.nqt + 3) / 4;
-  int64_t per_head = 0;
+  int64_t per_head = 0, per_class[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // items of groups = x mod 8
   for (int grp = 0; grp < ngroups; ++grp) {
     int olo, ohi;
-    if (group_offsets(g.Tq, g.Tk, g.nqt, 1 << 30, g.causal != 0, grp, olo, ohi))
-      per_head += (ohi - olo + 1 + seg - 1) / seg;
+    if (group_offsets(g.Tq, g.Tk, g.nqt, 1 << 30, g.causal != 0, grp, olo, ohi)) {
+      const int64_t n = (ohi - olo + 1 + seg - 1) / seg;
+      per_head += n;
+      per_class[grp % 8] += n;
+    }
   }
-  const int64_t items = per_xcd ? (BH + 7) / 8 * per_head : BH * per_head;
-  const int64_t k = (items + (per_xcd ? 4 : 32) - 1) / (per_xcd ? 4 : 32);
+  int64_t items = (BH + 7) / 8 * per_head;  // per-XCD mode: the most heads an XCD holds
+  if (!per_xcd) {
+    items = 0;
+    for (int c = 0; c < 8; ++c) items = per_class[c] > items ? per_class[c] : items;
+    items *= BH;
+  }
+  const int64_t k = (items + 3) / 4;
   kmax = (int)(k > 0 ? k : 1);
 }
 size_t screen_plan_bytes(const Geometry& g) {
