@@ -136,6 +136,9 @@ def test_long_bitmap_columns_forward_backward(causal, T, w):
         e = rel_err(got[name], want)
         _say(f"long columns: {name} rel err {e:.3e}")
         assert e <= TOL, f"{name}: rel err {e:.3e} > {TOL}"
+    for name, want, scale in (("dr", gref[3], P["dr_abs"]), ("dw", gref[4], P["dw_abs"])):
+        e = head_sum_err(got[name], want, scale)
+        assert e <= TOL, f"{name}: per-head error {e:.3e} > {TOL}"
 
 
 def test_trained_regime_forward_backward():

@@ -19,7 +19,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err
+from helpers import correlated_qkv, head_sum_err, np64, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +72,13 @@ def test_degenerate_forward_backward(name, dtype):
         else:
             e = rel_err(g, want)
             assert e <= tol, f"{nm}: rel err {e:.3e} > {tol}"
+    # dr, dw entry by entry, against the sum of each head's |terms| (a head
+    # with no terms must be exactly zero)
+    _, _, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), causal,
+                                        key_padding_mask=kpm_np)
+    for nm, got, want, scale in (("dr", dr, gref[3], P["dr_abs"]), ("dw", dw, gref[4], P["dw_abs"])):
+        e = head_sum_err(np64(got), want, scale)
+        assert e <= tol, f"{nm}: per-head error {e:.3e} > {tol}"
     for b in masked:
         assert torch.count_nonzero(y[b]) == 0
     if name == "r_huge":

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err
+from helpers import correlated_qkv, np64, rel_err, head_sum_err
 
 pytestmark = pytest.mark.gpu
 
@@ -64,3 +64,8 @@ def test_head_regime_forward_backward(regime, dtype):
         assert np.max(np.abs(want)) > 0, f"{name} vacuous"
         e = rel_err(np64(got), want)
         assert e <= tol, f"{name}: rel err {e:.3e} > {tol}"
+    # dr, dw entry by entry, against the sum of each head's |terms|
+    _, _, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), causal)
+    for name, got, want, scale in (("dr", dr, gref[3], P["dr_abs"]), ("dw", dw, gref[4], P["dw_abs"])):
+        e = head_sum_err(np64(got), want, scale)
+        assert e <= tol, f"{name}: per-head error {e:.3e} > {tol}"

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err
+from helpers import correlated_qkv, np64, rel_err, head_sum_err
 
 pytestmark = pytest.mark.gpu
 
@@ -44,6 +44,10 @@ def _check(B, Tq, Tk, H, D, dtype, causal, r, w, seed):
         assert np.max(np.abs(want)) > 0, f"{name} vacuous"
         e = rel_err(g_, want)
         assert e <= tol, f"{name}: rel err {e:.3e} > {tol}"
+    # dr, dw entry by entry, against the sum of each head's |terms|
+    for name, g_, want, scale in (("dr", got[4], gref[3], P["dr_abs"]), ("dw", got[5], gref[4], P["dw_abs"])):
+        e = head_sum_err(g_, want, scale)
+        assert e <= tol, f"{name}: per-head error {e:.3e} > {tol}"
     return P
 
 

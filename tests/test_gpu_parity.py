@@ -15,7 +15,7 @@ import torch
 
 import screening_oracle as O
 from helpers import (GOLDEN_ATTENTION, correlated_qkv, golden_inputs, golden_module, load_golden,
-                     np64, qkv, rel_err)
+                     head_sum_err, np64, qkv, rel_err)
 
 pytestmark = pytest.mark.gpu
 
@@ -133,6 +133,18 @@ def test_backward_parity(case, dtype):
         assert np.max(np.abs(want)) > 0, f"{name} vacuous"
         e = rel_err(np64(got), want)
         assert e <= tol, f"{name}: rel err {e:.3e} > {tol}"
+    _check_head_sums(q, k, v, r, w, dy, causal, kpm_np, None, dr, dw, ref, tol)
+
+
+def _check_head_sums(q, k, v, r, w, dy, causal, kpm_np, drop, dr, dw, ref, tol):
+    """dr and dw entry by entry: each head's error against the sum of its
+    terms' magnitudes (the live-pair oracle's dr_abs, dw_abs), so a head with
+    few or small terms is not hidden behind the largest one."""
+    _, _, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), np.array(r), np.array(w), np64(dy), causal,
+                                        key_padding_mask=kpm_np, dropout=drop)
+    for name, got, want, scale in (("dr", dr, ref[3], P["dr_abs"]), ("dw", dw, ref[4], P["dw_abs"])):
+        e = head_sum_err(np64(got), want, scale)
+        assert e <= tol, f"{name}: per-head error {e:.3e} > {tol}"
 
 
 # Attention dropout (attention.py:190): the kernels and the oracle share the
@@ -166,6 +178,7 @@ def test_dropout_parity(ci, dtype):
         assert np.max(np.abs(want)) > 0, f"{name} vacuous"
         e = rel_err(np64(got), want)
         assert e <= tol, f"{name}: rel err {e:.3e} > {tol}"
+    _check_head_sums(q, k, v, r, w, dy, causal, kpm_np, drop, grads[3], grads[4], ref, tol)
 
 
 def test_dropout_zero_is_identity_and_seed_reproduces():
