@@ -305,10 +305,10 @@ size_t screen_plan_bytes(const Geometry& g) {
 // vectors).  The live-unit bitmap must hold every pair with alpha > 0 (the
 // live and backward passes visit nothing else, and a missed pair's gradient
 // terms are linear in a = 1 - r(1-s)), so the vote's gate is lowered by that
-// bound.  Both inputs of 2-byte types screen in fp16, not bf16: u = 2^-12
-// instead of 2^-9, at the same MFMA rate, so the lowered gate admits about
-// 1% more 32x32 units instead of about 10% (measured on the configs[1]
-// inputs).  The operands are power-of-two scaled into fp16's normal range,
+// bound.  Both inputs of 2-byte types screen in fp16, not bf16: u = 2^-11
+// (11 significant bits) instead of 2^-8, so the lowered gate admits about
+// 2% more 32x32 units than hold a live pair instead of about 18% (counted on
+// the configs[1] inputs).  The operands are power-of-two scaled into fp16's normal range,
 // which keeps their values exact up to that rounding: K^ times 2^10 (its
 // components are at most 1, and down to 2^-24 stay normal), each raw query
 // row times the 2^e that puts its largest component in [2^10, 2^11) (bf16
@@ -323,7 +323,7 @@ using ScreenOp = typename std::conditional<sizeof(T) == 2, f16, float>::type;
 template <typename T>
 constexpr float kKhatScale = sizeof(T) == 2 ? 1024.0f : 1.0f;
 template <typename T>
-constexpr float kScreenSlack = sizeof(T) == 2 ? 2.441406e-4f + 1e-5f : 1e-5f;  // 2^-12 + 1e-5
+constexpr float kScreenSlack = sizeof(T) == 2 ? 4.8828125e-4f + 1e-5f : 1e-5f;  // 2^-11 + 1e-5
 
 // Power of two p with max|x| * p in [2^10, 2^11) (1 for a zero or non-finite
 // max): scales a query row into fp16's normal range exactly.

@@ -59,10 +59,11 @@ def _t_rel(got, ref, fro=True):
 
 # Width, in s, of the band below the threshold in which the screen may mark
 # a unit with no live pair: the 2-byte screen votes on K^ rounded to fp16
-# (|s_screen - s| <= 2^-12 sum_d |q^_d k^_d| <= 2^-12) against a gate lowered
-# by 2^-12 + 1e-5, so a marked unit's best pair has s > 1 - 1/r - 2^-11 - 1e-5
-# (fp32 accumulation inside the 1e-5).  Every unit with a live pair is marked.
-SCREEN_BAND = 2.0 ** -11 + 2e-5
+# (|s_screen - s| <= 2^-11 sum_d |q^_d k^_d| <= 2^-11, fp16's unit roundoff)
+# against a gate lowered by 2^-11 + 1e-5, so a marked unit's best pair has
+# s > 1 - 1/r - 2^-10 - 1e-5 (fp32 accumulation inside the 1e-5).  Every unit
+# with a live pair is marked.
+SCREEN_BAND = 2.0 ** -10 + 2e-5
 
 
 def _unit_map(bits, B, H, Tq, Tk):

@@ -270,9 +270,9 @@ def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
 
 # The vote's slack below the threshold 1 - 1/r, in s (kScreenSlack in
 # msa_fwd.hip): fp32 screens on fp32 K^; bf16 and fp16 screen on fp16 K^
-# (unit roundoff 2^-12), plus fp32 accumulation.
+# (unit roundoff 2^-11: 11 significant bits), plus fp32 accumulation.
 SLACK_F32 = 1e-5
-SLACK_16 = 2.0 ** -12 + 1e-5
+SLACK_16 = 2.0 ** -11 + 1e-5
 
 
 def _fp16_screen_units(q, k, r, w, causal):
