@@ -928,12 +928,17 @@ void fwd_live_kernel(FwdKArgs a) {
     for (int c = 0; c < NC; ++c) id[c] = ident_frag<T>(c, lane);
     // fp16: each lane's V row takes its 1/|v| before the transposes (in fp32,
     // rounded once to fp16: the value the transposed row would get), which
-    // holds one scale per lane instead of sixteen
+    // holds one scale per lane instead of sixteen.  The scheduling barriers
+    // keep the conversions in place: hoisted next to the S products they
+    // held 32 more values at once and spilled 9 VGPRs (live 42 -> 32 us at
+    // configs[1] in fp16 without the spill)
     if constexpr (kScaleRowsNotWeights<T>) {
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
         for (int e = 0; e < PER; ++e) vc[ks][e] = (T)((float)vc[ks][e] * ivl);
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int dblk = 0; dblk < NDH; ++dblk) {
