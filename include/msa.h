@@ -89,8 +89,12 @@ const char* msa_last_error(void);
 size_t msa_fwd_workspace_bytes(int B, int H, int Tq, int Tk, int D, int dtype);
 
 /* Number of uint32 words of the live-unit bitmap: one bit per
- * (b, h, 32-query unit, 32-key unit), set iff some in-window, unmasked pair of
- * the unit has alpha > 0.  With nqt = ceil(Tq/64), nkt = ceil(Tk/64), the
+ * (b, h, 32-query unit, 32-key unit), set for every unit in which some
+ * in-window, unmasked pair has alpha > 0, and otherwise only for units with
+ * such a pair whose s lies within the screen's slack below the threshold
+ * 1 - 1/r (2^-11 + 1e-5 for bf16 and fp16 inputs, 2^-10 + 1e-5 for fp32:
+ * the screen votes on fp16 operands); the live and backward passes give
+ * those pairs alpha = 0 exactly.  With nqt = ceil(Tq/64), nkt = ceil(Tk/64), the
  * (b, h) block holds 2*nqt rows (query unit qu: queries 32qu .. 32qu+31) of
  * ceil(2*nkt/32) words; key unit ku is bit ku%32 of word ku/32 of the row. */
 size_t msa_tile_bits_words(int B, int H, int Tq, int Tk);

@@ -578,6 +578,7 @@ struct PRow {
     for (int ks = 0; ks < NKS; ++ks)
       if (!(ok && KS * ks + PER * half < D)) f[ks] = M::zero();
   }
+  __device__ inline float get(int ks, int e) const { return M::get(f[ks], e); }
   __device__ inline float dot(const PRow& o) const {
     float s = 0.0f;
 #pragma unroll

@@ -10,8 +10,8 @@
 //                   reach the window's edges together.  Key tiles stream
 //                   global -> LDS by direct DMA into a ring (each tile is read
 //                   by the 4 waves in 4 consecutive steps).  Each wave forms
-//                   S^T = K^ Q^T on MFMA (raw bf16 Q, fp32 accumulation, scaled
-//                   by 1/|q_i|) and votes whether any in-window pair passes the
+//                   S^T = K^ Q^T on fp16 MFMA (the raw query rows rounded to
+//                   fp16, fp32 accumulation, scaled by 1/|q_i|) and votes whether any in-window pair passes the
 //                   trim-and-square threshold (attention.py:75-90).  Output:
 //                   the live-unit bitmap (32x32 units).
 //   fwd_live_kernel : one wave per 32-query unit; walks the unit's live bits,
@@ -299,31 +299,72 @@ size_t screen_plan_bytes(const Geometry& g) {
 }
 
 // ---------------------------------------------------------------------------
-// Screen operands.  The screen votes on S^T = K^ Q^T with K^ = k/|k| stored
-// in a 2-byte type for 2-byte inputs, so each vote sees s up to the rounding
-// of K^: |s_screen - s| <= u sum_d |q^_d k^_d| <= u (unit roundoff u, unit
-// vectors).  The live-unit bitmap must hold every pair with alpha > 0 (the
-// live and backward passes visit nothing else, and a missed pair's gradient
-// terms are linear in a = 1 - r(1-s)), so the vote's gate is lowered by that
-// bound.  Both inputs of 2-byte types screen in fp16, not bf16: u = 2^-11
-// (11 significant bits) instead of 2^-8, so the lowered gate admits about
-// 2% more 32x32 units than hold a live pair instead of about 18% (counted on
-// the configs[1] inputs).  The operands are power-of-two scaled into fp16's normal range,
-// which keeps their values exact up to that rounding: K^ times 2^10 (its
-// components are at most 1, and down to 2^-24 stay normal), each raw query
-// row times the 2^e that puts its largest component in [2^10, 2^11) (bf16
-// has 8 significant bits, so every component above 2^-24 of the largest is
-// exact in fp16).  fp32 inputs screen in fp32 (u = 2^-24 per K^ component).
+// Screen operands.  Every input type screens on fp16 MFMA operands: K^ =
+// k/|k| rounded to fp16, and each raw query row rounded to fp16, so each vote
+// sees s up to their rounding: |s_screen - s| <= (u_k + u_q + u_k u_q)
+// sum_d |q^_d k^_d| <= u_k + u_q + u_k u_q (unit roundoffs, unit vectors).
+// The live-unit bitmap must hold every pair with alpha > 0 (the live and
+// backward passes visit nothing else, and a missed pair's gradient terms are
+// linear in a = 1 - r(1-s)), so the vote's gate is lowered by that bound.
+// The operands are power-of-two scaled into fp16's normal range, which keeps
+// their rounding relative: K^ times 2^10 (its components are at most 1, and
+// down to 2^-24 stay normal), each raw query row times the 2^e that puts its
+// largest component in [2^10, 2^11) (components below 2^-24 of the largest
+// become subnormal: an absolute error of at most 2^-35 of |q| each).
+//   bf16 and fp16 inputs: the query rows are exact in fp16 (bf16 has 8
+//     significant bits, fp16 11), so u_q = 0 and u_k = 2^-11 (fp16 keeps 11
+//     significant bits).  fp16, not bf16 (u_k = 2^-8, at the same MFMA rate),
+//     because the lowered gate then admits about 2% more 32x32 units than
+//     hold a live pair instead of about 18% (counted on the configs[1]
+//     inputs).
+//   fp32 inputs: u_q = u_k = 2^-11, on the fp16 MFMA (16x the fp32 MFMA rate,
+//     a quarter of the operand bytes).
 // The vote's gate, in s, is 1 - 1/r - kScreenSlack, the slack covering the
 // rounding above, fp32 accumulation of D <= 128 products ((D+3) 2^-24) and
 // the fp32 1/|q| and 1/|k|.
 // ---------------------------------------------------------------------------
 template <typename T>
-using ScreenOp = typename std::conditional<sizeof(T) == 2, f16, float>::type;
+using ScreenOp = f16;
 template <typename T>
-constexpr float kKhatScale = sizeof(T) == 2 ? 1024.0f : 1.0f;
+constexpr float kKhatScale = 1024.0f;
 template <typename T>
-constexpr float kScreenSlack = sizeof(T) == 2 ? 4.8828125e-4f + 1e-5f : 1e-5f;  // 2^-11 + 1e-5
+constexpr float kScreenSlack = sizeof(T) == 2 ? 4.8828125e-4f + 1e-5f    // 2^-11 + 1e-5
+                                              : 9.765625e-4f + 1e-5f;    // 2^-10 + 1e-5
+
+// A query row of fp32 inputs in the 16-bit operand layout (the lane holds
+// elements KS*ks + PER*half + e, e < PER, as PRow<bf16, DP>), kept in fp32
+// until the screen rounds it to an fp16 operand.
+template <int DP>
+struct WideQueryRow {
+  static constexpr int KS = Mma<f16>::KS, PER = Mma<f16>::PER, NKS = DP / KS;
+  float f[NKS][PER];
+  __device__ inline void load(const float* p, bool ok, int D, int half) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = KS * ks + PER * half;
+      const bool in = ok && d0 < D;
+      const float* s = p + (d0 < D ? d0 : 0);
+#pragma unroll
+      for (int e = 0; e < PER; e += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(s + e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[ks][e + j] = in ? v[j] : 0.0f;
+      }
+    }
+  }
+  __device__ inline float get(int ks, int e) const { return f[ks][e]; }
+  __device__ inline float inv_norm(float eps) const {
+    float s = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) s += f[ks][e] * f[ks][e];
+    return inv_len(half_sum(s), eps);
+  }
+};
+// The screen's view of a raw query row: 2-byte rows as loaded, fp32 rows wide.
+template <typename T, int DP>
+using ScreenQueryRow = typename std::conditional<sizeof(T) == 2, PRow<T, DP>, WideQueryRow<DP>>::type;
 
 // Power of two p with max|x| * p in [2^10, 2^11) (1 for a zero or non-finite
 // max): scales a query row into fp16's normal range exactly.
@@ -485,7 +526,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // The own query rows (raw B operands) and the first key tiles' DMA need
   // only the item: they are issued first, and the head parameters and tile
   // ranges are formed while they are in flight.
-  PRow<T, DP> qrow[2];
+  ScreenQueryRow<T, DP> qrow[2];
 #pragma unroll
   for (int qh = 0; qh < 2; ++qh) {
     const int i = q0 + 32 * qh + l32;
@@ -538,14 +579,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   if (!wave_ok) { kt_lo = 0; kt_hi = -1; }
 
   // A-operand rows of key half kh: row 32kh + perm_row(l32), 16-byte chunk
-  // (KS*ks + PER*half)*sizeof(T)/16 = ks*KS*sizeof(T)/16 + half*PER*sizeof(T)/16
+  // (KS*ks + PER*half)*sizeof(S)/16 = ks*KS*sizeof(S)/16 + half*PER*sizeof(S)/16
   uint32_t aoff[2][NKS];
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int R = 32 * kh + perm_row(l32);
-      const int byte = (KS * ks + PER * half) * (int)sizeof(T);
+      const int byte = (KS * ks + PER * half) * (int)sizeof(S);
       aoff[kh][ks] = (uint32_t)(R * G::ROWB + ((((byte >> 4) ^ G::swz(R)) << 4) | (byte & 15)));
     }
 
@@ -558,18 +599,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[qh][r] = 0.0f;
-    if constexpr (sizeof(S) == 2) {
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
+    for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma_ng(kf[ks], qf[qh * NKS + ks], acc[qh]);
-      guard_frags(kf);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma(kf[ks], qf[qh * NKS + ks], acc[qh]);
-    }
+      for (int qh = 0; qh < 2; ++qh) acc[qh] = M::mma_ng(kf[ks], qf[qh * NKS + ks], acc[qh]);
+    guard_frags(kf);
   };
   // Threshold vote on key half kh of the tile at k0: a(s) is monotone in s and
   // s = acc/(|q_i| c_i) (c_i: the operands' power-of-two scales), so a 32x32
@@ -657,19 +691,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int e = 0; e < PER; ++e) mx = fmaxf(mx, fabsf(Mma<T>::get(qrow[qh].f[ks], e)));
-      const float c = sizeof(S) == 2 ? row_pow2(half_max(mx)) : 1.0f;
+        for (int e = 0; e < PER; ++e) mx = fmaxf(mx, fabsf(qrow[qh].get(ks, e)));
+      const float c = row_pow2(half_max(mx));
       qthr[qh] = vthr / qrow[qh].inv_norm(a.eps) * (c * kKhatScale<T>);
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        if constexpr (sizeof(S) == 2) {  // bf16 or fp16 rows, scaled by c into fp16
-          f32x16 t;
+      for (int ks = 0; ks < NKS; ++ks) {  // the row scaled by c, rounded to fp16
+        f32x16 t;
 #pragma unroll
-          for (int e = 0; e < PER; ++e) t[e] = Mma<T>::get(qrow[qh].f[ks], e) * c;
-          qf[qh * NKS + ks] = M::pack(t, 0);
-        } else {
-          qf[qh * NKS + ks] = qrow[qh].f[ks];
-        }
+        for (int e = 0; e < PER; ++e) t[e] = qrow[qh].get(ks, e) * c;
+        qf[qh * NKS + ks] = M::pack(t, 0);
       }
     }
   }
@@ -1017,7 +1047,7 @@ void fwd_live_kernel(FwdKArgs a) {
 }
 
 static int64_t khat_bytes(const Geometry& g) {
-  return round_up((int64_t)g.B * g.H * g.Tk_pad * g.DP * (int64_t)g.esize, 256);
+  return round_up((int64_t)g.B * g.H * g.Tk_pad * g.DP * (int64_t)sizeof(ScreenOp<float>), 256);  // fp16 rows
 }
 // Workspace: [K^][screen plan table]
 size_t fwd_ws_bytes(const Geometry& g) { return khat_bytes(g) + screen_plan_bytes(g); }

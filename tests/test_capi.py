@@ -44,8 +44,9 @@ def test_version_and_sizes():
     assert L.msa_tile_bits_words(4, 8, 8192, 8192) == 4 * 8 * 256 * 8
     assert L.msa_tile_bits_words(1, 1, 65, 65) == 4
     assert L.msa_tile_bits_words(1, 1, 64, 1100) == 2 * 2
-    # D=16 is padded to 32 in the workspace; one head, one item per lane at most
-    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 4 + 1024
+    # D=16 is padded to 32 in the workspace; one head, one item per lane at
+    # most; K^ is fp16 for every input type (fp32 inputs screen on fp16 too)
+    assert L.msa_fwd_workspace_bytes(1, 1, 64, 64, 16, 0) == 64 * 32 * 2 + 1024
     # fp16 takes bf16's sizes (2-byte elements)
     assert L.msa_fwd_workspace_bytes(4, 8, 8192, 8192, 64, 2) == one + 32 * 128 * 32
     # backward workspace: (dr, dw) partial per (b, h, 32-query unit), then dh

@@ -1,9 +1,9 @@
 """Long shapes on paths the short parity cases do not reach.
 
-* Five-slot key-tile ring: key tiles above 8 KiB (bf16 at D=128, fp32 at
-  D=64) stage through 5 LDS slots instead of 6.  At T=4096 a screen item
-  walks up to 40 steps, so the ring wraps many times inside the straight-line
-  loop.
+* Five-slot key-tile ring: key tiles above 8 KiB (D=128: the screen stages
+  fp16 K^ for every input type) stage through 5 LDS slots instead of 6.  At
+  T=4096 a screen item walks up to 40 steps, so the ring wraps many times
+  inside the straight-line loop.
 * Cross-attention with a long key side (Tq=64, Tk=70000, non-causal, window
   wider than Tk): each bitmap row holds 2188 key units, more than one 2048-unit
   row load, in the live pass and in dQ.
@@ -51,7 +51,7 @@ def _check(B, Tq, Tk, H, D, dtype, causal, r, w, seed):
     return P
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float32, 64)], ids=["bf16_D128", "f32_D64"])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float32, 128)], ids=["bf16_D128", "f32_D128"])
 def test_five_slot_ring_long_items(dtype, D):
     _check(1, 4096, 4096, 2, D, dtype, True, [1.2, 1.35], [3000.0, 700.0], seed=31)
 

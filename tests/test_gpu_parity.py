@@ -245,14 +245,15 @@ def test_backward_deterministic():
 ], ids=["bh4", "bh8", "bh72", "t2048"])
 def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
     # fp32: the bitmap holds every unit with a live pair, and beyond those only
-    # units with a pair within the vote's slack (1e-5 in s) below the threshold
+    # units with a pair within BAND_F32 below the threshold (the vote's slack
+    # plus the same bound again for the rounding of the values it votes on)
     D = 64
     q, k, v = correlated_qkv(B, T, T, H, D, seed=4, dtype=torch.float32, rho=0.3)
     y, hnorm, bits = _run_fwd(q, k, v, r, w, True)
     # the bitmap is kept per 32x32 unit: 2*nqt rows of ceil(2*nkt/32) words
     rr = np.array(r)
     nW, nA, act = O.tile_counts(np64(q), np64(k), rr, np.array(w), True, tile=32)
-    _, _, band = O.tile_counts(np64(q), np64(k), 1.0 / (1.0 / rr + SLACK_F32), np.array(w), True, tile=32)
+    _, _, band = O.tile_counts(np64(q), np64(k), 1.0 / (1.0 / rr + BAND_F32), np.array(w), True, tile=32)
     _, nA64, act64 = O.tile_counts(np64(q), np64(k), rr, np.array(w), True, tile=64)
     nqu = nku = T // 32
     words = (nku + 31) // 32
@@ -269,9 +270,11 @@ def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
 
 
 # The vote's slack below the threshold 1 - 1/r, in s (kScreenSlack in
-# msa_fwd.hip): fp32 screens on fp32 K^; bf16 and fp16 screen on fp16 K^
-# (unit roundoff 2^-11: 11 significant bits), plus fp32 accumulation.
-SLACK_F32 = 1e-5
+# msa_fwd.hip): every type screens on fp16 K^ (unit roundoff 2^-11: 11
+# significant bits); fp32 query rows are rounded to fp16 as well (another
+# 2^-11), 2-byte ones are exact in fp16; plus fp32 accumulation.
+SLACK_F32 = 2.0 ** -10 + 1e-5
+BAND_F32 = 2.0 * SLACK_F32
 SLACK_16 = 2.0 ** -11 + 1e-5
 
 
