@@ -323,10 +323,8 @@ size_t screen_plan_bytes(const Geometry& g) {
 // rounding above, fp32 accumulation of D <= 128 products ((D+3) 2^-24) and
 // the fp32 1/|q| and 1/|k|.
 // ---------------------------------------------------------------------------
-template <typename T>
-using ScreenOp = f16;
-template <typename T>
-constexpr float kKhatScale = 1024.0f;
+using ScreenOp = f16;              // the screen's MFMA operand type
+constexpr float kKhatScale = 1024.0f;  // K^ is stored times 2^10
 template <typename T>
 constexpr float kScreenSlack = sizeof(T) == 2 ? 4.8828125e-4f + 1e-5f    // 2^-11 + 1e-5
                                               : 9.765625e-4f + 1e-5f;    // 2^-10 + 1e-5
@@ -410,10 +408,10 @@ __global__ __launch_bounds__(256) void prep_k_kernel(PrepKArgs a) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss += x[u][e] * x[u][e];
     ss = group_sum<CPR>(ss);  // the row's CPR lanes
-    float inv = kKhatScale<T> / fmaxf(sqrtf(ss), a.eps);
+    float inv = kKhatScale / fmaxf(sqrtf(ss), a.eps);
     if (t >= a.Tk || (a.kpm != nullptr && a.kpm[(int64_t)b * a.Tk + t])) inv = 0.0f;
     if (t < a.Tk_pad) {
-      ScreenOp<T>* p = (ScreenOp<T>*)a.khat + ((int64_t)bh * a.Tk_pad + t) * DP + d0;
+      ScreenOp* p = (ScreenOp*)a.khat + ((int64_t)bh * a.Tk_pad + t) * DP + d0;
 #pragma unroll
       for (int e = 0; e < VEC; e += 4)
         store4(p + e, x[u][e] * inv, x[u][e + 1] * inv, x[u][e + 2] * inv, x[u][e + 3] * inv);
@@ -492,7 +490,7 @@ __device__ inline int ceil_tiles(int x) { return -floor_tiles(-x); }
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void fwd_screen_kernel(FwdKArgs a) {
-  using S = ScreenOp<T>;  // operand type of the screen's MFMAs
+  using S = ScreenOp;  // operand type of the screen's MFMAs
   using M = Mma<S>;
   using frag = typename M::frag;
   using G = ScreenTile<S, DP>;
@@ -693,7 +691,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
         for (int e = 0; e < PER; ++e) mx = fmaxf(mx, fabsf(qrow[qh].get(ks, e)));
       const float c = row_pow2(half_max(mx));
-      qthr[qh] = vthr / qrow[qh].inv_norm(a.eps) * (c * kKhatScale<T>);
+      qthr[qh] = vthr / qrow[qh].inv_norm(a.eps) * (c * kKhatScale);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {  // the row scaled by c, rounded to fp16
         f32x16 t;
@@ -1047,7 +1045,7 @@ void fwd_live_kernel(FwdKArgs a) {
 }
 
 static int64_t khat_bytes(const Geometry& g) {
-  return round_up((int64_t)g.B * g.H * g.Tk_pad * g.DP * (int64_t)sizeof(ScreenOp<float>), 256);  // fp16 rows
+  return round_up((int64_t)g.B * g.H * g.Tk_pad * g.DP * (int64_t)sizeof(ScreenOp), 256);  // fp16 rows
 }
 // Workspace: [K^][screen plan table]
 size_t fwd_ws_bytes(const Geometry& g) { return khat_bytes(g) + screen_plan_bytes(g); }
