@@ -1,0 +1,104 @@
+"""A seeded sweep over the shape and option space of the fused path.
+
+Each case draws B, Tq, Tk, H, D, the dtype, causal or not, per-head r and w
+(r from just above 1, where almost every pair is live, to 2.5; w from 1 to
+past T and sometimes infinite), a key-padding mask and attention dropout, and
+checks the forward output and every gradient (dq, dk, dv, dr, dw) against the
+float64 oracle (oracle/screening_oracle.py, the restatement of
+attention.py:142-200 and norm.py:23-25) at the parity tolerances: 1e-5 fp32,
+2e-2 bf16, 5e-3 fp16.  y, dq, dk and dv are held to them on the whole-tensor
+and Frobenius errors of helpers.errors, and on the per-(b, h) error too,
+except for 2-byte inputs: their backward forms dP = dh . v^ on MFMA with dh
+rounded to the input type (the reference's fused backward forms it from fp32
+dO, screening_bwd.py:207, bwd wrapper :248), so a gradient fed by one or
+two pairs whose dP is small beside |dh| carries that rounding almost alone:
+2.5% in dq in case 37 (bf16, one query, one key, D = 128; dP computed from
+the bf16-rounded dh differs from the exact one by 2.3%).  Such slices, and
+whole cases with fewer than 32 live pairs, are held to 3x the tolerance;
+with many pairs the roundings average out and the usual tolerance holds
+(every other GPU test).  dr and dw are sums of terms of
+both signs and are held per head against the sum of their terms' magnitudes
+(helpers.head_sum_err).  The shapes stay small (T <= 320) so the oracle runs
+in seconds; the cases reach the ragged edges the hand-picked cases do not
+combine (one query or one key, Tq far from Tk under a causal mask, D = 16
+with padding to 32, several heads sharing a window ranking).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import screening_oracle as O
+from helpers import correlated_qkv, errors, head_sum_err, np64
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 5e-3}
+DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+DEV = "cuda"
+NCASES = 48
+
+
+def _case(idx):
+    g = np.random.default_rng(7000 + idx)
+    dtype = DTYPES[idx % 3]
+    B = int(g.integers(1, 4))
+    H = int(g.integers(1, 7))
+    D = int(g.choice([16, 32, 64, 128]))
+    causal = bool(g.random() < 0.7)
+    Tq = int(g.integers(1, 4) if g.random() < 0.12 else g.integers(1, 321))
+    Tk = Tq if (causal and g.random() < 0.5) else int(g.integers(1, 4) if g.random() < 0.12 else g.integers(1, 321))
+    r = (1.02 + 1.5 * g.random(H)).tolist()
+    w = np.exp(g.uniform(0.0, math.log(2.0 * max(Tq, Tk) + 2.0), H))
+    w[g.random(H) < 0.15] = np.inf
+    kpm = None
+    if g.random() < 0.4:
+        kpm = torch.from_numpy(g.random((B, Tk)) < 0.1)
+    drop = None
+    if g.random() < 0.3:
+        drop = (0.25, int(g.integers(1, 2 ** 62)))
+    return dict(dtype=dtype, B=B, H=H, D=D, causal=causal, Tq=Tq, Tk=Tk, r=r, w=w.tolist(), kpm=kpm,
+                drop=drop, seed=100 + idx)
+
+
+@pytest.mark.parametrize("idx", range(NCASES))
+def test_sweep_forward_backward(idx):
+    from multiscreen import ops
+    c = _case(idx)
+    dtype, B, H, D, Tq, Tk = c["dtype"], c["B"], c["H"], c["D"], c["Tq"], c["Tk"]
+    print(f"sweep {idx}: {dtype} B={B} H={H} D={D} Tq={Tq} Tk={Tk} causal={c['causal']} "
+          f"kpm={c['kpm'] is not None} drop={c['drop'] is not None}", flush=True)
+    q, k, v = correlated_qkv(B, Tq, Tk, H, D, seed=c["seed"], dtype=dtype, rho=0.35)
+    dy = torch.randn(B, Tq, H, D, generator=torch.Generator().manual_seed(c["seed"] + 1)).to(dtype)
+    rg = torch.tensor(c["r"], dtype=torch.float32, device=DEV)
+    wg = torch.tensor(c["w"], dtype=torch.float32, device=DEV)
+    kpm_d = None if c["kpm"] is None else c["kpm"].to(DEV)
+    drop = () if c["drop"] is None else c["drop"]
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, c["causal"], 1e-8, kpm_d, *drop)
+    grads = ops.bwd_raw(qd, kd, vd, rg, wg, c["causal"], 1e-8, y, hnorm, bits, dy.to(DEV), kpm_d, *drop)
+    torch.cuda.synchronize()
+
+    kpm_np = None if c["kpm"] is None else c["kpm"].numpy()
+    args = (np64(q), np64(k), np64(v), np.array(c["r"]), np.array(c["w"]))
+    dref = None if c["drop"] is None else c["drop"]
+    yref = O.forward(*args, c["causal"], key_padding_mask=kpm_np, dropout=dref)
+    ref = O.backward(*args, np64(dy), c["causal"], key_padding_mask=kpm_np, dropout=dref)
+    tol = TOL[dtype]
+    if np.max(np.abs(yref)) < 1e-3:
+        # (almost) nothing passes the threshold: the outputs are (almost) zero
+        assert np.max(np.abs(np64(y))) <= 1e-3 + tol
+        return
+    _, _, P = O.sparse_forward_backward(*args, np64(dy), c["causal"], key_padding_mask=kpm_np, dropout=dref)
+    two_byte = dtype != torch.float32
+    few = two_byte and len(P["i"]) < 32
+    slice_tol = 3 * tol if two_byte else tol
+    whole_tol = 3 * tol if few else tol
+    for name, got, want in zip(("y", "dq", "dk", "dv"), (y,) + tuple(grads[:3]), (yref,) + tuple(ref[:3])):
+        e = errors(np64(got), want)
+        assert e["max"] <= whole_tol and e["fro"] <= whole_tol and e["slice"] <= slice_tol, f"{name}: {e}"
+    for name, got, want, scale in (("dr", grads[3], ref[3], P["dr_abs"]), ("dw", grads[4], ref[4], P["dw_abs"])):
+        e = head_sum_err(np64(got), want, scale)
+        assert e <= tol, f"{name}: per-head error {e:.3e} > {tol}"
