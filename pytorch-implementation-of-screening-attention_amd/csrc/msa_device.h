@@ -378,12 +378,6 @@ __device__ inline float softmask(int dd, float iw) {
   const float x = (float)(-dd) * iw;
   return 0.5f * (cospif(x) + 1.0f);
 }
-__device__ inline float softmask_dw(int dd, float iw) {
-  // d/dw [ (cos(pi rel/w)+1)/2 ] = sin(pi rel/w) * pi * rel / (2 w^2),  rel = j - i
-  const float rel = (float)(-dd);
-  const float x = rel * iw;
-  return 0.5f * sinpif(x) * 3.14159265358979f * rel * iw * iw;
-}
 
 // max(x[l], x[l ^ 32]) in every lane (as half_sum, with max).
 __device__ inline float half_max(float x) {
@@ -512,21 +506,6 @@ __device__ inline void load_chunk(const float* p, float (&x)[4]) {
   for (int e = 0; e < 4; ++e) x[e] = v[e];
 }
 
-// Loads 4 consecutive values as fp32.
-__device__ inline f32x4 load4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
-__device__ inline f32x4 load4(const bf16* p) {
-  bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
-  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-}
-__device__ inline f32x4 load4(const f16* p) {
-  f16x4 v = *reinterpret_cast<const f16x4*>(p);
-  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-}
-
-__device__ inline int64_t floordiv(int64_t a, int64_t b) {  // b > 0
-  return a >= 0 ? a / b : -((-a + b - 1) / b);
-}
-
 // 1/max(sqrt(ss), eps) from a squared length, by the hardware reciprocal
 // square root (v_rsq_f32, ~1 ulp): min(rsq(ss), 1/eps) is the same clamp
 // (rsq(0) = +inf).
@@ -616,16 +595,6 @@ __device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]
 template <int N>
 __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
 
-// Block barrier for LDS hand-over that leaves vector memory traffic (e.g. DMA
-// prefetches into other buffers) in flight: this wave's LDS operations
-// complete, then s_barrier.  The asm statements keep the compiler from moving
-// memory operations across it.
-__device__ inline void block_sync_lds() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Waits for this wave's LDS traffic and keeps the compiler from moving
 // memory operations across the point (LDS ops of one wave run in order).
 __device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -648,95 +617,6 @@ __device__ inline int lds_swz(int R) {
   else if constexpr (CPR == 8) return b1 | (b3 << 1) | ((b0 ^ b2) << 2);
   else return b1 | (b3 << 1) | ((b0 ^ b2) << 2) | (b0 << 3);
 }
-
-// ---------------------------------------------------------------------------
-// Row tiles staged global -> LDS by direct DMA (global_load_lds, 16 bytes a
-// lane, no register round trip).  LDS tile: ROWS rows of DP elements,
-// row-major, with the 16-byte chunks of row R XOR-swizzled by lds_swz (below)
-// so that operand reads under perm_row are free of bank conflicts.  NT threads (a block, or one wave
-// staging its own half tile) share a tile: thread t moves chunks
-// c = u*NT + t.  The per-thread source offsets are planned once (plan()); a
-// tile that runs past the tensor's last row reads that row instead (slow
-// path, last tile only), and columns past D read the row's first chunk;
-// consumers mask both.
-// ---------------------------------------------------------------------------
-template <typename T, int DP, int ROWS = 64, int NT = 256>
-struct StageTile {
-  static constexpr int ROWB = DP * (int)sizeof(T);  // bytes per row
-  static constexpr int CPR = ROWB / 16;             // 16-byte chunks per row (4..32)
-  static constexpr int TILEB = ROWS * ROWB;         // bytes per tile
-  static constexpr int CPT = ROWS * CPR / NT;       // chunks per thread
-  __device__ static inline int swz(int R) { return lds_swz<CPR>(R); }
-  // byte offset of element d of row R
-  __device__ static inline int off(int R, int d) {
-    const int byte = d * (int)sizeof(T);
-    return R * ROWB + ((((byte >> 4) ^ swz(R)) << 4) | (byte & 15));
-  }
-  __device__ static inline void chunk(int u, int t, int D, int& R, int& col) {
-    const int c = u * NT + t;
-    R = c / CPR;
-    col = (((c % CPR) ^ swz(R)) * 16) / (int)sizeof(T);
-    if (col >= D) col = 0;
-  }
-  // Per-thread byte offsets (row R of the tile at R*st) of its chunks, as
-  // unsigned 32-bit values: a uniform 64-bit base plus one 32-bit lane offset
-  // is the DMA's scalar-base addressing form.  Valid while a tile spans less
-  // than 2^31 bytes (planned(st)); issue() takes the general path otherwise.
-  struct Plan {
-    uint32_t off[CPT];
-  };
-  __device__ static inline bool planned(int64_t st) {
-    return st >= 0 && st * ROWS * (int64_t)sizeof(T) < ((int64_t)1 << 31);
-  }
-  __device__ static inline Plan plan(int64_t st, int D, int t) {
-    Plan p;
-#pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-      int R, col;
-      chunk(u, t, D, R, col);
-      p.off[u] = (uint32_t)((R * st + col) * (int64_t)sizeof(T));
-    }
-    return p;
-  }
-  // DMA rows r0 .. r0+ROWS-1 of a tensor whose row r starts at row0 + r*st
-  // (nrows >= 1 rows, D valid columns) into `lds`.  `grp` (wave index for a
-  // block-wide stager, 0 for a wave stager) must be wave-uniform: the LDS
-  // destination of one instruction is a uniform base.
-  __device__ static inline void issue(const Plan& pl, const T* row0, int64_t st, int64_t r0, int64_t nrows, int D,
-                                      char* lds, int t, int grp) {
-    const T* base = row0 + r0 * st;
-    if (r0 + ROWS <= nrows && planned(st)) {
-#pragma unroll
-      for (int u = 0; u < CPT; ++u)
-        __builtin_amdgcn_global_load_lds(
-            (const void __attribute__((address_space(1)))*)((const char*)base + (uint64_t)pl.off[u]),
-            (void __attribute__((address_space(3)))*)(lds + (u * NT + grp * 64) * 16), 16, 0, 0);
-    } else {
-#pragma unroll
-      for (int u = 0; u < CPT; ++u) {
-        int R, col;
-        chunk(u, t, D, R, col);
-        const int64_t row = r0 + R < nrows ? R : nrows - 1 - r0;
-        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(base + row * st + col),
-                                         (void __attribute__((address_space(3)))*)(lds + (u * NT + grp * 64) * 16),
-                                         16, 0, 0);
-      }
-    }
-  }
-  // A/B operand fragment: row R, slots d = KS*ks + PER*half + e.  Rows need
-  // no mask here (every consumer zeroes their scale factors or weights);
-  // columns past D exist only when DP = 32 holds D = 16, and read as zero.
-  __device__ static inline typename Mma<T>::frag frag(const char* lds, int R, int ks, int half, int D) {
-    const int d0 = Mma<T>::KS * ks + Mma<T>::PER * half;
-    const typename Mma<T>::frag f = Mma<T>::load((const T*)(lds + off(R, d0)));
-    if constexpr (DP == 32) return d0 < D ? f : Mma<T>::zero();
-    else return f;
-  }
-};
-// A wave staging its own 32-row half tile into its own buffer (no block
-// barrier needed).
-template <typename T, int DP>
-using WaveStage = StageTile<T, DP, 32, 64>;
 
 // Set bits lo..hi of one bitmap row (position u = bit u%32 of word u/32),
 // visited in increasing order.  Lane l holds word w0 + l, so one load round
@@ -881,22 +761,6 @@ __device__ inline void xcd_interleave_ranked(const float* r, const float* w, int
   by = b * H + h;
   rh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rraw), h));
   wh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wraw), h));
-}
-
-// XCD-aware block order.  Blocks are dispatched round-robin over the 8 XCDs
-// in linear order (x fastest); when the grid divides evenly, remap so each
-// XCD receives a contiguous run of logical blocks (the query tiles of the same
-// heads share that XCD's L2).  Logical x is reversed so the longest causal
-// rows start first.
-__device__ inline void xcd_order(int& bx, int& by) {
-  const int nx = gridDim.x, N = gridDim.x * gridDim.y;
-  int p = blockIdx.x + nx * blockIdx.y;
-  if ((N & 7) == 0) {
-    const int per = N >> 3;
-    p = (p & 7) * per + (p >> 3);
-  }
-  by = p / nx;
-  bx = nx - 1 - (p - by * nx);
 }
 
 }  // namespace msa
