@@ -175,7 +175,7 @@ __device__ inline void chunk_partial(const DecArgs& a, int b, int h, const HeadP
       const int64_t j = base + u * KPW + kl;
       if (j < cend && av > 0.0f) {
         // every lane of the key's group takes this branch together
-        const float m = softmask((int)(pos - j), hp.iw);
+        const float m = mask_fast((int)(pos - j), hp.w, hp.iw);
         const vec vv = *reinterpret_cast<const vec*>(vb + j * a.vs.st);
         const float vs2 = group_sum<LPK>(V::dot(vv, vv, 0.0f));
         const float coef = av * av * m * inv_len(vs2, a.eps);

@@ -325,24 +325,39 @@ __device__ inline float sinpi_poly(float t, float u) {  // u = t^2
   return c * t;
 }
 // Soft mask m = (cos(pi dd/w) + 1)/2 (attention.py:114) for an in-window
-// distance (|dd| < w, so |dd/w| < 1); out of the window the value is finite
-// and the caller masks it.
-__device__ inline float mask_fast(int dd, float iw) {
-  const float y = fminf(fabsf((float)dd * iw), 1.0f);
-  const float t = fminf(y, 1.0f - y);
-  const float c = cospi_poly(t * t);
-  return 0.5f + 0.5f * (y > 0.5f ? -c : c);
+// distance (|dd| < w, so y = |dd|/w < 1); out of the window the value is
+// finite and the caller masks it.  For y <= 1/2, m = 1/2 + cos(pi y)/2 (both
+// terms at least 0: no cancellation).  Past 1/2, m falls to 0 at the window's
+// edge and that form would cancel, and y = |dd| (1/w) would carry the
+// rounding of 1/w into 1 - y; there m = sin^2(pi t/2) with t = 1 - y formed
+// as (w - |dd|) / w, whose numerator is exact in fp32 (w/2 <= |dd| <= w:
+// Sterbenz), so m keeps a few ulps of relative accuracy down to the last
+// in-window distance.  t also gives sin(pi y) = sin(pi t) for dm/dw.
+struct MaskArg {
+  float y, t;  // |dd|/w, and min(y, 1 - y) with 1 - y = (w - |dd|)/w
+  bool far;    // y > 1/2
+};
+__device__ inline MaskArg mask_arg(int dd, float w, float iw) {
+  MaskArg a;
+  const float ad = fabsf((float)dd);
+  a.y = fminf(ad * iw, 1.0f);
+  a.far = a.y > 0.5f;
+  a.t = a.far ? fmaxf((w - ad) * iw, 0.0f) : a.y;
+  return a;
 }
+__device__ inline float mask_of(const MaskArg& a) {
+  const float z = 0.5f * a.t;  // sin(pi t/2) for the far half
+  const float sz = sinpi_poly(z, z * z);
+  const float c = cospi_poly(a.t * a.t);
+  return a.far ? sz * sz : 0.5f + 0.5f * c;
+}
+__device__ inline float mask_fast(int dd, float w, float iw) { return mask_of(mask_arg(dd, w, iw)); }
 // The same mask and dm/dw = (pi/2) dd sin(pi dd/w) / w^2 (the w-derivative
 // of (cos(pi (j-i)/w) + 1)/2, attention.py:114).
-__device__ inline void mask_fast_dw(int dd, float iw, float& m, float& dm) {
-  const float x = fminf(fmaxf((float)dd * iw, -1.0f), 1.0f);
-  const float y = fabsf(x);
-  const float t = fminf(y, 1.0f - y);
-  const float u = t * t;
-  const float c = cospi_poly(u);
-  m = 0.5f + 0.5f * (y > 0.5f ? -c : c);
-  const float sn = copysignf(sinpi_poly(t, u), x);
+__device__ inline void mask_fast_dw(int dd, float w, float iw, float& m, float& dm) {
+  const MaskArg a = mask_arg(dd, w, iw);
+  m = mask_of(a);
+  const float sn = copysignf(sinpi_poly(a.t, a.t * a.t), (float)dd);
   dm = (0.5f * 3.14159265358979f) * (float)dd * sn * iw * iw;
 }
 
@@ -361,23 +376,16 @@ __device__ inline void unit_mask_table(float* mt, float* mdt, int dmin, const He
   const bool in = lane < 63 && in_window(dd, hp);
   if constexpr (kDw) {
     float m, dm;
-    mask_fast_dw(dd, hp.iw, m, dm);
+    mask_fast_dw(dd, hp.w, hp.iw, m, dm);
     mt[lane] = in ? m : 0.0f;
     mdt[lane] = in ? dm : 0.0f;
   } else {
-    mt[lane] = in ? mask_fast(dd, hp.iw) : 0.0f;
+    mt[lane] = in ? mask_fast(dd, hp.w, hp.iw) : 0.0f;
   }
 }
 
 // Trim-and-square pre-square value a = 1 - r (1 - s)  (attention.py:90).
 __device__ inline float trim(float s, float r) { return 1.0f - r * (1.0f - s); }
-
-// Cosine soft mask m = (cos(pi (j-i)/w) + 1)/2 (attention.py:114) and its
-// derivative with respect to w, for an in-window distance dd = i - j.
-__device__ inline float softmask(int dd, float iw) {
-  const float x = (float)(-dd) * iw;
-  return 0.5f * (cospif(x) + 1.0f);
-}
 
 // max(x[l], x[l ^ 32]) in every lane (as half_sum, with max).
 __device__ inline float half_max(float x) {

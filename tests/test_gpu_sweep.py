@@ -14,14 +14,22 @@ dO, screening_bwd.py:207, bwd wrapper :248), so a gradient fed by one or
 two pairs whose dP is small beside |dh| carries that rounding almost alone:
 2.5% in dq in case 37 (bf16, one query, one key, D = 128; dP computed from
 the bf16-rounded dh differs from the exact one by 2.3%).  Such slices, and
-whole cases with fewer than 32 live pairs, are held to 3x the tolerance;
-with many pairs the roundings average out and the usual tolerance holds
-(every other GPU test).  dr and dw are sums of terms of
-both signs and are held per head against the sum of their terms' magnitudes
+whole cases with fewer than 32 live pairs (their dr and dw too), are held to
+3x the tolerance; with many pairs the roundings average out and the usual
+tolerance holds (every other GPU test).  dr and dw are sums of terms of both
+signs and are held per head against the sum of their terms' magnitudes
 (helpers.head_sum_err).  The shapes stay small (T <= 320) so the oracle runs
 in seconds; the cases reach the ragged edges the hand-picked cases do not
 combine (one query or one key, Tq far from Tk under a causal mask, D = 16
 with padding to 32, several heads sharing a window ranking).
+
+The same generator over seeds 48..399 (352 more cases, run once) found no
+other kind of error: five fp32 cases exceed the per-slice tolerance (1.0e-5
+to 5.5e-5) in a slice at about 1% of its tensor's largest value whose row
+holds one live pair just above the threshold (a = 1 - r(1 - s) of 0.008 to
+0.06), where alpha = a^2 turns a few fp32 ulps of s into that relative error
+(2r/a of 80 to 450 times the error of s); and one fp16 one-pair case is the
+dh rounding above.
 """
 
 import math
@@ -101,4 +109,4 @@ def test_sweep_forward_backward(idx):
         assert e["max"] <= whole_tol and e["fro"] <= whole_tol and e["slice"] <= slice_tol, f"{name}: {e}"
     for name, got, want, scale in (("dr", grads[3], ref[3], P["dr_abs"]), ("dw", grads[4], ref[4], P["dw_abs"])):
         e = head_sum_err(np64(got), want, scale)
-        assert e <= tol, f"{name}: per-head error {e:.3e} > {tol}"
+        assert e <= whole_tol, f"{name}: per-head error {e:.3e} > {whole_tol}"
