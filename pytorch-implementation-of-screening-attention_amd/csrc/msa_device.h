@@ -704,18 +704,22 @@ struct ColWalk {
 
 // Balanced XCD mapping for kernels with one block per (tile, head).  Blocks
 // are dispatched round-robin over the 8 XCDs in linear order (x fastest).
-// With nx % 8 == 0, XCD x receives tiles x, x+8, x+16, ... of every head,
-// head after head: each XCD gets an equal share of every head's rows (whose
-// cost depends on the head's window and threshold), and the blocks it runs
-// at one time cover a few heads, so neighbouring tiles share its L2.  Within
-// a head the highest tiles come first.
+// With nx % 32 == 0, XCD x receives the runs of four adjacent tiles 4x..4x+3,
+// 4x+32.., ... of every head, head after head (with nx % 8 == 0 only, tiles
+// x, x+8, ...): each XCD gets an equal share of every head's rows (whose cost
+// depends on the head's window and threshold), and the blocks it runs at one
+// time cover a few heads.  Adjacent tiles walk nearly the same key rows one
+// unit apart, so within a run the rows one block loads are still in the
+// XCD's L2 when the next block needs them.  Within a head the highest tiles
+// come first.
 __device__ inline void xcd_interleave(int& bx, int& by) {
   const int nx = gridDim.x;
   if ((nx & 7) == 0) {
     const int p = blockIdx.x + nx * blockIdx.y;
     const int x = p & 7, s = p >> 3, per = nx >> 3;
     by = s / per;
-    bx = nx - 1 - ((s - by * per) * 8 + x);
+    const int t = s - by * per;  // the block's place in XCD x's share of the head
+    bx = nx - 1 - ((nx & 31) == 0 ? (t >> 2) * 32 + x * 4 + (t & 3) : t * 8 + x);
   } else {
     by = blockIdx.y;
     bx = nx - 1 - blockIdx.x;
