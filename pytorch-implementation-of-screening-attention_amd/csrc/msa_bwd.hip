@@ -370,23 +370,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
       }
     }
     // dq^T[d][i] += sum_j K^T[d][j] (ds/|k|)^T[j][i], K^T by identity from
-    // the key rows, one 32-column block of d at a time
-    // (fp16: the K rows take 1/|k| instead)
+    // the key rows, one 32-column block of d at a time (fp16: K^T takes
+    // 1/|k| instead, below)
     if constexpr (!kScaleRowsNotWeights<T>) {
       float ksc[16];
       read_row_scales(sk, half, ksc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] *= ksc[r];
-    } else {
-      // fp16: each lane's K row takes its 1/|k| before the transposes (in
-      // fp32, rounded once to fp16: the value the transposed row would get),
-      // one scale per lane instead of sixteen (after the guard: S read these
-      // registers)
-      guard_frags(kc);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int e = 0; e < PER; ++e) kc[ks][e] = (T)((float)kc[ks][e] * ikl);
     }
     frag db[NC];
 #pragma unroll
@@ -402,6 +392,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) ==
       for (int r = 0; r < 16; ++r) tr[r] = 0.0f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) tr = M::mma_ng(kc[dblk * NC + c], id[c], tr);
+      if constexpr (kScaleRowsNotWeights<T>) scale_rows_fp32(tr, sk, half);
 #pragma unroll
       for (int c = 0; c < NC; ++c) kt[c] = M::pack(tr, c * PER);
 #pragma unroll
@@ -635,22 +626,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
         for (int r = 0; r < 16; ++r) body(r);
       }
     }
-    // ds/|q|; fp16: each lane's Q row takes its 1/|q| instead, before the
-    // transposes (in fp32, rounded once to fp16: the value the transposed row
-    // would get), one scale per lane instead of sixteen (after the guard: S
-    // read these registers)
+    // ds/|q| (fp16: Q^T takes 1/|q| instead, below)
     if constexpr (!kScaleRowsNotWeights<T>) {
       float qsc[16];
       read_row_scales(sq, half, qsc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] *= qsc[r];
-    } else {
-      const float iqm = sq[m];
-      guard_frags(qf);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int e = 0; e < PER; ++e) qf[ks][e] = (T)((float)qf[ks][e] * iqm);
     }
     // dv^T[d][j] += sum_i dH^T[d][i] P[i][j];  dk^T[d][j] += sum_i Q^T[d][i] (ds/|q|)[i][j]
     // with dH^T, Q^T from identity products on the row registers, one
@@ -673,6 +654,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(bwd_waves<T,
 #pragma unroll
         for (int c = 0; c < NC; ++c)
           tr = M::mma_ng(op == 0 ? hf[dblk * NC + c] : qf[dblk * NC + c], id[c], tr);
+        if constexpr (kScaleRowsNotWeights<T>)
+          if (op == 1) scale_rows_fp32(tr, sq, half);
 #pragma unroll
         for (int c = 0; c < NC; ++c) t[c] = M::pack(tr, c * PER);
 #pragma unroll

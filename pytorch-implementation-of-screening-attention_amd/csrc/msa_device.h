@@ -598,6 +598,19 @@ __device__ inline void read_row_scales(const float* sc, int half, float (&o)[16]
     }
 }
 
+// fp16 row scaling of an identity-MFMA transpose: c holds the raw rows
+// exactly in fp32 (products with 1, sums with 0), register r row
+// 16*(r/8) + 8*half + r%8, and each register takes its row's factor in fp32;
+// the operand pack then rounds once to fp16.  The same value as scaling the
+// row registers before the transpose, at one multiply per register instead
+// of a convert, multiply and convert per element.
+__device__ inline void scale_rows_fp32(f32x16& c, const float* sc, int half) {
+  float f[16];
+  read_row_scales(sc, half, f);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) c[r] *= f[r];
+}
+
 // Waits until at most N of this wave's vector memory operations (loads,
 // stores and global->LDS DMA) are outstanding.
 template <int N>
