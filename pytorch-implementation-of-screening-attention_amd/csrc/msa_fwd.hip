@@ -14,7 +14,8 @@
 //                   fp16, fp32 accumulation, scaled by 1/|q_i|) and votes whether any in-window pair passes the
 //                   trim-and-square threshold (attention.py:75-90).  Output:
 //                   the live-unit bitmap (32x32 units).
-//   fwd_live_kernel : one wave per 32-query unit; walks the unit's live bits,
+//   fwd_live_kernel : one wave per 32-query unit (S waves for launches with few
+//                   units, each taking every S-th live unit); walks the unit's live bits,
 //                   recomputes S^T from the raw K rows (exact products, fp32
 //                   1/|k|) for those key units only, forms alpha*m
 //                   (attention.py:92-119) and accumulates H^T += V^T P^T with
@@ -780,19 +781,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // on the raw V rows.  The
 // epilogue applies TanhNorm (norm.py:23-25) and writes y in (B,T,H,D) and |h|
 // per row.  Units with no live key unit get y = 0, |h| = 0.
+// S > 1 (launches with fewer rows than the chip has wave slots): S waves per
+// row in one block, wave w taking the row's live units w, w+S, ...; waves
+// 1..S-1 hand their partial H^T to wave 0 through LDS, which adds them in
+// wave order (fixed, so results repeat bitwise) and runs the epilogue.
 // ---------------------------------------------------------------------------
-template <typename T, int DP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : 1)))
+template <typename T, int DP, int S>
+__global__ __launch_bounds__(64 * S)
+__attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && DP <= 64 ? 3 : (S > 1 ? (DP <= 32 ? 3 : 2) : 1))))
 void fwd_live_kernel(FwdKArgs a) {
   using M = Mma<T>;
   using frag = typename M::frag;
   using R = PRow<T, DP>;
   constexpr int KS = M::KS, PER = M::PER, NKS = DP / KS, NDH = DP / 32, NC = 32 / KS;
-  __shared__ __attribute__((aligned(16))) float sk[32];  // 1/|k_j| (0 if padded or masked) of the current unit
-  __shared__ __attribute__((aligned(16))) float sv[32];  // 1/|v_j| of the current unit's key rows
-  __shared__ float mt[64];  // soft-mask table of the current unit (unit_mask_table)
-  __shared__ frag qsh[NKS][kWave];  // own raw q operand fragments
-  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  // per wave:
+  __shared__ __attribute__((aligned(16))) float sk_w[S][32];  // 1/|k_j| (0 if padded or masked) of the current unit
+  __shared__ __attribute__((aligned(16))) float sv_w[S][32];  // 1/|v_j| of the current unit's key rows
+  __shared__ float mt_w[S][64];  // soft-mask table of the current unit (unit_mask_table)
+  // own raw q operand fragments; with S > 1 the same bytes then take the
+  // wave's partial H^T for wave 0 (after the wave's last read of its q)
+  constexpr int kQshBytes = NKS * kWave * (int)sizeof(frag);
+  constexpr int kPartBytes = NDH * 16 * kWave * 4;
+  constexpr int kWaveBytes = S > 1 && kPartBytes > kQshBytes ? kPartBytes : kQshBytes;
+  __shared__ __attribute__((aligned(16))) char wbuf[S][kWaveBytes];
+  const int lane = (int)(threadIdx.x & 63), half = lane >> 5, l32 = lane & 31;
+  const int wave = S > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
+  float* sk = sk_w[wave];
+  float* sv = sv_w[wave];
+  float* mt = mt_w[wave];
+  frag (&qsh)[NKS][kWave] = *reinterpret_cast<frag(*)[NKS][kWave]>(wbuf[wave]);
   int qu, bh;
   float head_r, head_w;
   xcd_interleave_ranked(a.r, a.w, a.H, qu, bh, head_r, head_w);
@@ -813,7 +830,8 @@ void fwd_live_kernel(FwdKArgs a) {
   const uint32_t* brow = a.bits + ((int64_t)bh * 2 * a.nqt + qu) * a.nku_words;
   RowWalk walk(brow, ku_lo, ku_hi);
   int cur = walk.next();
-  if (cur < 0) {  // wave-uniform: no live key unit, y = 0 and |h| = 0
+  if (cur < 0) {  // block-uniform: no live key unit, y = 0 and |h| = 0
+    if (wave != 0) return;
     if (valid) {
       if (half == 0) a.hnorm[(int64_t)bh * a.Tq + i] = 0.0f;
 #pragma unroll
@@ -861,6 +879,11 @@ void fwd_live_kernel(FwdKArgs a) {
         if (KS * ks >= a.D) f[ks] = M::zero();
     }
   };
+  // S > 1: this wave's first unit is the row's live unit number `wave` (a
+  // wave left without one loads the row's first unit's rows and skips the
+  // loop)
+  const int first = cur;
+  for (int w = 0; w < wave && cur >= 0; ++w) cur = walk.next();
   // own queries as raw B operands (lane -> query), kept in LDS and read back
   // per unit (the registers go to the unit rows), and 1/|q_i|; their loads
   // go first, the first unit's behind them
@@ -870,9 +893,10 @@ void fwd_live_kernel(FwdKArgs a) {
   {
     R qr;
     qr.load((const T*)a.q + b * a.qs.sb + (int64_t)(valid ? i : 0) * a.qs.st + h * a.qs.sh, valid, a.D, half);
-    load_k(cur, kc);
-    load_v(cur, vc);
-    kok = key_ok(cur);
+    const int u0 = cur >= 0 ? cur : first;
+    load_k(u0, kc);
+    load_v(u0, vc);
+    kok = key_ok(u0);
     iq = qr.inv_norm(a.eps);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qsh[ks][lane] = qr.f[ks];
@@ -884,7 +908,7 @@ void fwd_live_kernel(FwdKArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dblk][r] = 0.0f;
 
-  for (;;) {
+  while (cur >= 0) {
     const int k0 = cur * kUnit;
     // S^T = K Q^T on the raw rows (exact products of the inputs, fp32
     // accumulation), scaled by 1/|k_j| in fp32 below: register r -> key
@@ -918,7 +942,11 @@ void fwd_live_kernel(FwdKArgs a) {
     // free, so those loads run behind the rest of this unit's work (past the
     // last unit, the current one again, a cache hit: every iteration then
     // waits for the same count)
-    const int nxt = walk.next();
+    int nxt = -1;  // this wave's next unit: S positions on in the row's walk
+    for (int w = 0; w < S; ++w) {
+      nxt = walk.next();
+      if (nxt < 0) break;
+    }
     const int nl = nxt >= 0 ? nxt : cur;
     const bool kok_c = kok;
     load_k(nl, kc);
@@ -1028,6 +1056,23 @@ void fwd_live_kernel(FwdKArgs a) {
     cur = nxt;
   }
 
+  if constexpr (S > 1) {
+    // waves 1..S-1 hand their H^T to wave 0 (each in its own wbuf row),
+    // which adds them in wave order
+    auto part = [&](int w) { return reinterpret_cast<float(*)[kWave]>(wbuf[w]); };
+    if (wave > 0)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part(wave)[dblk * 16 + r][lane] = o[dblk][r];
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w = 1; w < S; ++w)
+#pragma unroll
+      for (int dblk = 0; dblk < NDH; ++dblk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dblk][r] += part(w)[dblk * 16 + r][lane];
+  }
   // TanhNorm per query row (lane -> query, registers -> d), y in (B,T,H,D)
   float ss = 0.0f;
 #pragma unroll
@@ -1047,6 +1092,10 @@ void fwd_live_kernel(FwdKArgs a) {
 static int64_t khat_bytes(const Geometry& g) {
   return round_up((int64_t)g.B * g.H * g.Tk_pad * g.DP * (int64_t)sizeof(ScreenOp), 256);  // fp16 rows
 }
+// Rows (32-query units) below which the live pass splits each row's units
+// over several waves: about two waves per SIMD of the chip.
+constexpr int64_t kLiveSplitWaves = 2048;
+
 // Workspace: [K^][screen plan table]
 size_t fwd_ws_bytes(const Geometry& g) { return khat_bytes(g) + screen_plan_bytes(g); }
 
@@ -1088,9 +1137,22 @@ static hipError_t launch_fwd_t(const FwdCall& c) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  // A launch with few rows (under about two waves per SIMD) splits each
+  // row's live units over S waves (DP <= 64: the S waves' LDS fits)
+  const int64_t rows = (int64_t)2 * g.nqt * g.B * g.H;
+  const int S = DP > 64 ? 1 : (rows * 4 <= kLiveSplitWaves ? 4 : (rows * 2 <= kLiveSplitWaves ? 2 : 1));
+  const dim3 grid((unsigned)(2 * g.nqt), (unsigned)(g.B * g.H));
   timer_begin(3, c.stream);
-  hipLaunchKernelGGL((fwd_live_kernel<T, DP>), dim3((unsigned)(2 * g.nqt), (unsigned)(g.B * g.H)), dim3(64), 0,
-                     c.stream, fa);
+  if constexpr (DP <= 64) {
+    if (S == 4)
+      hipLaunchKernelGGL((fwd_live_kernel<T, DP, 4>), grid, dim3(256), 0, c.stream, fa);
+    else if (S == 2)
+      hipLaunchKernelGGL((fwd_live_kernel<T, DP, 2>), grid, dim3(128), 0, c.stream, fa);
+    else
+      hipLaunchKernelGGL((fwd_live_kernel<T, DP, 1>), grid, dim3(64), 0, c.stream, fa);
+  } else {
+    hipLaunchKernelGGL((fwd_live_kernel<T, DP, 1>), grid, dim3(64), 0, c.stream, fa);
+  }
   timer_end(3, c.stream);
   return hipGetLastError();
 }
