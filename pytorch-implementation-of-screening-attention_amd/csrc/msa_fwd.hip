@@ -781,8 +781,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // on the raw V rows.  The
 // epilogue applies TanhNorm (norm.py:23-25) and writes y in (B,T,H,D) and |h|
 // per row.  Units with no live key unit get y = 0, |h| = 0.
-// S > 1 (launches with fewer rows than the chip has wave slots): S waves per
-// row in one block, wave w taking the row's live units w, w+S, ...; waves
+// S > 1 (launches with at most kLiveSplitWaves / S rows, D <= 64): S waves
+// per row in one block, wave w taking the row's live units w, w+S, ...; waves
 // 1..S-1 hand their partial H^T to wave 0 through LDS, which adds them in
 // wave order (fixed, so results repeat bitwise) and runs the epilogue.
 // ---------------------------------------------------------------------------
