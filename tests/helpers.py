@@ -106,6 +106,14 @@ def np64(t):
     return t.detach().cpu().double().numpy()
 
 
+def rw64(x):
+    """Per-head r or w as the kernels receive them (fp32 device arrays),
+    widened to float64 for the oracle.  Near a window edge the fp32 rounding
+    of w matters: at w = 1 + 3e-4, dm/dw of the pair at |i - j| = 1 is
+    proportional to w - 1, which fp32(w) shifts by 2e-4 relative."""
+    return np.asarray(x, dtype=np.float32).astype(np.float64)
+
+
 def load_golden(name):
     return np.load(os.path.join(GOLDEN, f"{name}.npz"))
 

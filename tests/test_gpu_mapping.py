@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, head_sum_err, np64, rel_err
+from helpers import correlated_qkv, head_sum_err, np64, rel_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -44,7 +44,7 @@ def test_mapping_branches(case):
     y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None)
     dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dy.to(DEV))
     torch.cuda.synchronize()
-    args = (np64(q), np64(k), np64(v), np.array(r), np.array(w))
+    args = (np64(q), np64(k), np64(v), rw64(r), rw64(w))
     yref = O.forward(*args, causal)
     ref = O.backward(*args, np64(dy), causal)
     assert np.max(np.abs(yref)) > 1e-3, "vacuous case"
