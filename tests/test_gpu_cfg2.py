@@ -23,7 +23,7 @@ import torch
 
 import bench
 import screening_oracle as O
-from helpers import errors, head_sum_err, np64, rel_err
+from helpers import errors, head_sum_err, np64, rel_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -67,7 +67,7 @@ def test_cfg2_full_shape_forward_backward(variant):
     got = {n: np64(t) for n, t in zip(("y", "dq", "dk", "dv", "dr", "dw"), (y, dq, dk, dv, dr, dw))}
     units = _unit_bits(bits, B, H, T)
     del qd, kd, vd, dyd, y, hnorm, bits, dq, dk, dv
-    rr, ww = np.array(r, dtype=np.float64), np.array(w, dtype=np.float64)
+    rr, ww = rw64(r), rw64(w)
     yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), True)
     _say(f"cfg2: oracle done, {len(P['i'])} live pairs")
     assert len(P["i"]) > (50000 if variant == "sharpened" else 2000)
@@ -129,7 +129,7 @@ def test_long_bitmap_columns_forward_backward(causal, T, w):
         lo = ku if causal else max(0, ku - int(np.ceil(w[h_] / 32)))
         span = max(span, int(qus.max()) - lo)
     assert span >= 256, span
-    yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), np.array(r), np.array(w), np64(dy), causal)
+    yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rw64(r), rw64(w), np64(dy), causal)
     _say(f"long columns: {len(P['i'])} live pairs, widest column reach {span} units")
     for name, want in zip(("y", "dq", "dk", "dv", "dr", "dw"), (yref,) + tuple(gref)):
         assert np.max(np.abs(want)) > 0, f"{name} vacuous"
@@ -158,7 +158,7 @@ def test_trained_regime_forward_backward():
     torch.cuda.synchronize()
     got = {n: np64(t) for n, t in zip(("y", "dq", "dk", "dv", "dr", "dw"), (y, dq, dk, dv, dr, dw))}
     units = _unit_bits(bits, B, H, T)
-    rr, ww = np.array(r, dtype=np.float64), np.array(w, dtype=np.float64)
+    rr, ww = rw64(r), rw64(w)
     yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), True)
     window = sum(min(i + 1, int(np.ceil(w_))) for w_ in w for i in range(T)) * B
     frac = len(P["i"]) / window

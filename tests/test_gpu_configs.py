@@ -31,7 +31,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import errors, head_sum_err, np64, rel_err
+from helpers import errors, head_sum_err, np64, rel_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -104,7 +104,7 @@ def test_cfg4_long_prefill_all_rows_bf16():
     got = np64(y)
     units = _unit_map(bits, B, H, T, T)
     del y, hnorm, bits
-    rr, ww = np.array(r), np.array(w)
+    rr, ww = rw64(r), rw64(w)
     # one candidate pass at the band's lower edge (s > 1 - 1/r - band) gives
     # both the band's pairs and, filtered exactly, the live pairs
     r_band = 1.0 / (1.0 / rr + SCREEN_BAND)

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err
+from helpers import correlated_qkv, np64, rel_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -33,6 +33,6 @@ def test_decode_head_dims(D, dtype):
         split = ops.decode_step(qd, kc, vc, L, rg, wg, window_hint=10 ** 6)
         torch.cuda.synchronize()
         assert torch.equal(single, split), L
-        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, np.array(r), np.array(w))
+        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, rw64(r), rw64(w))
         assert np.max(np.abs(ref)) > 0
         assert rel_err(np64(split), ref, heads=(0, 1)) <= TOL[dtype], L

@@ -19,7 +19,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, head_sum_err, np64, rel_err
+from helpers import correlated_qkv, head_sum_err, np64, rel_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -60,7 +60,7 @@ def test_degenerate_forward_backward(name, dtype):
     dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dyd, kpm_d)
     torch.cuda.synchronize()
     kpm_np = None if kpm is None else kpm.numpy()
-    rr, ww = np.array(r, dtype=np.float64), np.array(w, dtype=np.float64)
+    rr, ww = rw64(r), rw64(w)
     yref = O.forward(np64(q), np64(k), np64(v), rr, ww, causal, key_padding_mask=kpm_np)
     gref = O.backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), causal, key_padding_mask=kpm_np)
     tol = TOL[dtype]
@@ -109,7 +109,7 @@ def test_zero_and_tiny_rows(dtype):
     y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None)
     dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dyd)
     torch.cuda.synchronize()
-    rr, ww = np.array(r), np.array(w)
+    rr, ww = rw64(r), rw64(w)
     yref = O.forward(np64(q), np64(k), np64(v), rr, ww, causal)
     gref = O.backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), causal)
     for nm, got, want in zip(("y", "dq", "dk", "dv", "dr", "dw"), (y, dq, dk, dv, dr, dw), (yref,) + tuple(gref)):

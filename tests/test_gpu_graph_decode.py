@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err
+from helpers import correlated_qkv, np64, rel_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +49,7 @@ def test_decode_at_matches_decode_for_every_launch_shape():
             got = ops.decode_step_at(qd, kc, vc, pos, rg, wg, window_hint=hint)
             assert torch.equal(got, base), (L, hint)
             assert torch.equal(ops.decode_step(qd, kc, vc, L, rg, wg, window_hint=hint), base), (L, hint)
-        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, np.array(r), np.array(w))
+        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, rw64(r), rw64(w))
         assert rel_err(np64(base), ref, heads=(0, 1)) <= 2e-2, L
     # a position past the capacity reads as the full cache
     qd = q[:, T - 1].to(DEV)

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err, head_sum_err
+from helpers import correlated_qkv, np64, rel_err, head_sum_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +56,7 @@ def test_head_regime_forward_backward(regime, dtype):
     y, hnorm, bits = ops.fwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, None)
     dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dyd)
     torch.cuda.synchronize()
-    rr, ww = np.array(r), np.array(w)
+    rr, ww = rw64(r), rw64(w)
     yref = O.forward(np64(q), np64(k), np64(v), rr, ww, causal)
     gref = O.backward(np64(q), np64(k), np64(v), rr, ww, np64(dy), causal)
     tol = TOL[dtype]

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err, head_sum_err
+from helpers import correlated_qkv, np64, rel_err, head_sum_err, rw64
 
 pytestmark = pytest.mark.gpu
 
@@ -36,7 +36,7 @@ def _check(B, Tq, Tk, H, D, dtype, causal, r, w, seed):
     dq, dk, dv, dr, dw = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dyd)
     torch.cuda.synchronize()
     got = [np64(t) for t in (y, dq, dk, dv, dr, dw)]
-    yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), np.array(r), np.array(w),
+    yref, gref, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rw64(r), rw64(w),
                                               np64(dy), causal)
     print(f"long: {len(P['i'])} live pairs", flush=True)
     tol = TOL[dtype]

@@ -15,7 +15,7 @@ import torch
 
 import screening_oracle as O
 from helpers import (GOLDEN_ATTENTION, correlated_qkv, golden_inputs, golden_module, load_golden,
-                     head_sum_err, np64, qkv, rel_err)
+                     head_sum_err, np64, qkv, rel_err, rw64)
 
 pytestmark = pytest.mark.gpu
 
@@ -101,7 +101,7 @@ def test_forward_parity(case, dtype):
     q, k, v, kpm = _case_inputs(case, dtype)
     y, hnorm, bits = _run_fwd(q, k, v, r, w, causal, kpm)
     kpm_np = None if kpm is None else kpm.numpy()
-    yref, href = O.forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), causal,
+    yref, href = O.forward(np64(q), np64(k), np64(v), rw64(r), rw64(w), causal,
                            key_padding_mask=kpm_np, return_h=True)
     assert np.max(np.abs(yref)) > 1e-3, "vacuous case"
     assert rel_err(np64(y), yref) <= TOL[dtype]
@@ -126,7 +126,7 @@ def test_backward_parity(case, dtype):
     kpm_np = None if kpm is None else kpm.numpy()
     # the backward differentiates the kernel's own forward output y, so the
     # oracle is fed the same dy
-    ref = O.backward(np64(q), np64(k), np64(v), np.array(r), np.array(w), np64(dy), causal,
+    ref = O.backward(np64(q), np64(k), np64(v), rw64(r), rw64(w), np64(dy), causal,
                      key_padding_mask=kpm_np)
     tol = TOL[dtype]
     for name, got, want in zip(("dq", "dk", "dv", "dr", "dw"), (dq, dk, dv, dr, dw), ref):
@@ -140,7 +140,7 @@ def _check_head_sums(q, k, v, r, w, dy, causal, kpm_np, drop, dr, dw, ref, tol):
     """dr and dw entry by entry: each head's error against the sum of its
     terms' magnitudes (the live-pair oracle's dr_abs, dw_abs), so a head with
     few or small terms is not hidden behind the largest one."""
-    _, _, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), np.array(r), np.array(w), np64(dy), causal,
+    _, _, P = O.sparse_forward_backward(np64(q), np64(k), np64(v), rw64(r), rw64(w), np64(dy), causal,
                                         key_padding_mask=kpm_np, dropout=drop)
     for name, got, want, scale in (("dr", dr, ref[3], P["dr_abs"]), ("dw", dw, ref[4], P["dw_abs"])):
         e = head_sum_err(np64(got), want, scale)
@@ -166,7 +166,7 @@ def test_dropout_parity(ci, dtype):
     grads = ops.bwd_raw(qd, kd, vd, rg, wg, causal, 1e-8, y, hnorm, bits, dy.to(DEV), kpm_d, *drop)
     torch.cuda.synchronize()
     kpm_np = None if kpm is None else kpm.numpy()
-    args = (np64(q), np64(k), np64(v), np.array(r), np.array(w))
+    args = (np64(q), np64(k), np64(v), rw64(r), rw64(w))
     yref = O.forward(*args, causal, key_padding_mask=kpm_np, dropout=drop)
     ref = O.backward(*args, np64(dy), causal, key_padding_mask=kpm_np, dropout=drop)
     tol = TOL[dtype]
@@ -251,10 +251,10 @@ def test_tile_bitmap_matches_oracle_counts(B, T, H, r, w):
     q, k, v = correlated_qkv(B, T, T, H, D, seed=4, dtype=torch.float32, rho=0.3)
     y, hnorm, bits = _run_fwd(q, k, v, r, w, True)
     # the bitmap is kept per 32x32 unit: 2*nqt rows of ceil(2*nkt/32) words
-    rr = np.array(r)
-    nW, nA, act = O.tile_counts(np64(q), np64(k), rr, np.array(w), True, tile=32)
-    _, _, band = O.tile_counts(np64(q), np64(k), 1.0 / (1.0 / rr + BAND_F32), np.array(w), True, tile=32)
-    _, nA64, act64 = O.tile_counts(np64(q), np64(k), rr, np.array(w), True, tile=64)
+    rr = rw64(r)
+    nW, nA, act = O.tile_counts(np64(q), np64(k), rr, rw64(w), True, tile=32)
+    _, _, band = O.tile_counts(np64(q), np64(k), 1.0 / (1.0 / rr + BAND_F32), rw64(w), True, tile=32)
+    _, nA64, act64 = O.tile_counts(np64(q), np64(k), rr, rw64(w), True, tile=64)
     nqu = nku = T // 32
     words = (nku + 31) // 32
     b = bits.cpu().numpy().view(np.uint32).reshape(B, H, nqu, words)
@@ -363,7 +363,7 @@ def test_decode_matches_forward_rows(dtype):
     ops = _ops()
     rg, wg = _rw(H, r, w)
     kc, vc = k.to(DEV), v.to(DEV)
-    yfull = O.forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), True)
+    yfull = O.forward(np64(q), np64(k), np64(v), rw64(r), rw64(w), True)
     for L in (1, 2, 64, 257, 700):
         y = ops.decode_step(q[:, L - 1].to(DEV), kc, vc, L, rg, wg)
         torch.cuda.synchronize()
@@ -387,7 +387,7 @@ def test_decode_window_hint_changes_only_the_grid():
         base = ops.decode_step(qd, kc, vc, L, rg, wg)
         for hint in (1, 2048, math.ceil(max(w)), 10 ** 6):
             assert torch.equal(ops.decode_step(qd, kc, vc, L, rg, wg, window_hint=hint), base), (L, hint)
-        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, np.array(r), np.array(w))
+        ref = O.decode_row(np64(q[:, L - 1]), np64(k), np64(v), L, rw64(r), rw64(w))
         assert rel_err(np64(base), ref, heads=(0, 1)) <= 2e-2, L
 
 
@@ -428,7 +428,7 @@ def test_cfg2_full_size_sampled_rows_bf16():
     r[0], r[1] = 1.15, 1.3
     y = _run_fwd(q, k, v, r, w, True)[0]
     rows = [0, 1, 63, 64, 1000, 4095, 4096, 8191]
-    yref = O.rows_forward(np64(q), np64(k), np64(v), np.array(r), np.array(w), rows, True)
+    yref = O.rows_forward(np64(q), np64(k), np64(v), rw64(r), rw64(w), rows, True)
     assert np.max(np.abs(yref)) > 1e-3
     assert rel_err(np64(y[:, rows]), yref) <= 2e-2
 

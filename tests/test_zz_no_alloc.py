@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import screening_oracle as O
-from helpers import correlated_qkv, np64, rel_err
+from helpers import correlated_qkv, np64, rel_err, rw64
 
 TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
 
@@ -68,7 +68,7 @@ def test_decode_noalloc_matches_decode_on_consecutive_calls():
         got = _decode(L, qd, kc, vc, n, rg, wg, hint, static=True)
         torch.cuda.synchronize()
         assert torch.equal(got, want), (B, T, H, D, n)
-        ref = O.decode_row(np64(q[:, n - 1]), np64(k), np64(v), n, np.array(r), np.array(w))
+        ref = O.decode_row(np64(q[:, n - 1]), np64(k), np64(v), n, rw64(r), rw64(w))
         assert np.max(np.abs(ref)) > 1e-3
         assert rel_err(np64(got), ref, heads=(0, 1)) <= TOL[dtype]
 
